@@ -1,0 +1,372 @@
+"""CPU oracle for the AWQ W4A16 linear path (test infrastructure, never product).
+
+This module restates, in numpy and CPU torch, the arithmetic of SGLite's AWQ
+linear path so that the HIP engine can be checked against it.  Only the test
+suite, the package smoke check and the benchmark's CPU-baseline leg import it;
+the product path never does.
+
+Reference functions restated here (paths relative to
+``python/sglite/srt/model_executor/``):
+
+* nibble order      -- layers/quantization/awq_triton.py:53-62 (reverse order
+                       [0,4,1,5,2,6,3,7] and shifts = 4*order) and
+                       layers/quantization/marlin_utils.py:249-282, 340-347
+                       (unpack_cols + argsort([0,2,4,6,1,3,5,7])).
+* dequantisation    -- layers/quantization/awq_triton.py:99-101, 119-122:
+                       W = ((q >> s) & 0xF  -  (z >> s) & 0xF) * scale, with the
+                       group row = k // group_size, one rounding to the output
+                       dtype.
+* GEMM              -- layers/quantization/awq.py:133-147 and
+                       awq_triton.py:144-195: y = x @ W, then ``+ bias`` in the
+                       activation dtype.  The contract accumulates in fp32 (the
+                       Marlin path's ``use_fp32_reduce=True``,
+                       marlin_utils.py:16, 408), not the Triton fallback's fp16.
+* fused MoE         -- layers/fused_moe/fused.py:11-31 (softmax top-k and
+                       renormalisation), fused.py:101-202 (GEMM1, silu_and_mul
+                       with the gate half first, GEMM2 times the routed weight
+                       in fp32, sum over top-k), kernels/triton/fused_moe.py:
+                       7-50 and 174-178.
+
+How each part is pinned (tests/test_oracle.py):
+  unpack/pack         KAT words (0x76543210 -> [0,4,1,5,2,6,3,7],
+                      [0..7] -> 0x75316420), a literal simulation of the
+                      Triton kernel's triple ``interleave`` + shifts, and a
+                      literal restatement of the Marlin unpack + argsort path.
+  dequantize          exhaustive (q, z) x scale sweep against numpy's float16
+                      rounding of the float64 product (fp16) and a bit-level
+                      round-to-nearest-even (bf16); q == z gives 0; z=0, s=1
+                      gives q; s = 2^-g pins the group mapping.
+  awq_gemm            float64 brute force on tiny shapes; exact integer
+                      products with s=1, z=0; one-hot rows give rows of W.
+  repack/unrepack     round trip on random and ragged shapes; the repacked
+                      dequantisation equals ``dequantize``.
+  MoE                 explicit per-(token, slot) loops against the vectorised
+                      form; softmax/top-k are torch's textbook routines.
+The reference's own tests are not shipped (its .gitignore lists ``tests``), so
+no reference golden vectors exist for this path.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+# Nibble p of a packed int32 holds logical column 8j + AWQ_ORDER[p]
+# (marlin_utils.py:340-347 undoes exactly this interleave).
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+# Logical column 8j + i lives in nibble REVERSE_AWQ_ORDER[i]
+# (awq_triton.py:53-62: reverse order [0,4,1,5,2,6,3,7], shift = 4 * order).
+REVERSE_AWQ_ORDER = (0, 4, 1, 5, 2, 6, 3, 7)
+
+_DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _as_u32(a) -> np.ndarray:
+    if isinstance(a, torch.Tensor):
+        a = a.cpu().numpy()
+    return np.ascontiguousarray(a).astype(np.int64).astype(np.uint32)
+
+
+def unpack_awq(packed) -> np.ndarray:
+    """Unpack AWQ int32 words [R, C/8] into logical 4-bit values [R, C] (int32).
+
+    q[r, 8j+i] = (packed[r, j] >> 4*REVERSE_AWQ_ORDER[i]) & 0xF
+    (awq_triton.py:53-62, 119-120; the shift is logical here, which equals the
+    reference's arithmetic shift after the & 0xF mask).
+    """
+    p = _as_u32(packed)
+    R, C8 = p.shape
+    out = np.empty((R, C8, 8), dtype=np.int32)
+    for i in range(8):
+        out[:, :, i] = ((p >> np.uint32(4 * REVERSE_AWQ_ORDER[i])) & np.uint32(0xF)).astype(np.int32)
+    return out.reshape(R, C8 * 8)
+
+
+def pack_awq(q) -> np.ndarray:
+    """Pack logical 4-bit values [R, C] into AWQ int32 words [R, C/8].
+
+    Inverse of :func:`unpack_awq`: nibble p receives column 8j + AWQ_ORDER[p].
+    """
+    if isinstance(q, torch.Tensor):
+        q = q.cpu().numpy()
+    q = np.asarray(q).astype(np.uint32)
+    R, C = q.shape
+    if C % 8:
+        raise ValueError("column count must be a multiple of 8")
+    q = q.reshape(R, C // 8, 8)
+    w = np.zeros((R, C // 8), dtype=np.uint32)
+    for p in range(8):
+        w |= (q[:, :, AWQ_ORDER[p]] & np.uint32(0xF)) << np.uint32(4 * p)
+    return w.view(np.int32)
+
+
+def resolve_group_size(group_size: int, K: int) -> int:
+    """Group size -1 means one group over all of K (awq_marlin.py:182-184)."""
+    return K if group_size == -1 else group_size
+
+
+def dequantize(qweight, qzeros, scales: torch.Tensor, group_size: Optional[int] = None) -> torch.Tensor:
+    """Dequantise AWQ tensors to W[K, N] in ``scales.dtype``.
+
+    W[k, n] = rnd((q[k, n] - z[k // G, n]) * s[k // G, n])   (awq_triton.py:119-122)
+
+    q - z is an exact integer in [-15, 15]; its product with an fp16 or bf16
+    scale is exact in float64, so rounding the float64 product once to the
+    output dtype is the single round-to-nearest-even of the reference.
+    ``group_size`` defaults to K // qzeros.shape[0] (awq_triton.py:155-157).
+    """
+    q = unpack_awq(qweight)
+    z = unpack_awq(qzeros)
+    K, N = q.shape
+    if group_size is None:
+        group_size = K // z.shape[0]
+    G = resolve_group_size(group_size, K)
+    g_of_k = np.arange(K) // G
+    s = scales.detach().cpu().to(torch.float64).numpy()
+    diff = (q - z[g_of_k, :]).astype(np.float64)
+    w64 = diff * s[g_of_k, :]
+    return torch.from_numpy(w64).to(scales.dtype)
+
+
+def awq_gemm(x: torch.Tensor, qweight, qzeros, scales: torch.Tensor, bias: Optional[torch.Tensor] = None,
+             group_size: Optional[int] = None) -> torch.Tensor:
+    """fp32-accumulated AWQ linear: y = rnd(x @ W) (+ bias in the activation dtype).
+
+    Mirrors awq.py:133-147 (reshape to [M, K], GEMM, ``out + bias``, reshape to
+    x.shape[:-1] + (N,)) with the accumulation done in fp32 as in the Marlin
+    path (marlin_utils.py:408).
+    """
+    W = dequantize(qweight, qzeros, scales, group_size)
+    K, N = W.shape
+    x2 = x.detach().cpu().reshape(-1, K)
+    y = (x2.float() @ W.float()).to(x.dtype)
+    if bias is not None:
+        y = y + bias.detach().cpu().to(y.dtype)
+    return y.reshape(*x.shape[:-1], N)
+
+
+def awq_gemm_f64(x: torch.Tensor, qweight, qzeros, scales: torch.Tensor, group_size: Optional[int] = None) -> np.ndarray:
+    """Brute-force float64 product x @ W with W from :func:`dequantize` (tiny shapes only)."""
+    W = dequantize(qweight, qzeros, scales, group_size).to(torch.float64).numpy()
+    xs = x.detach().cpu().to(torch.float64).numpy().reshape(-1, W.shape[0])
+    M, K = xs.shape
+    N = W.shape[1]
+    out = np.zeros((M, N), dtype=np.float64)
+    for m in range(M):
+        for k in range(K):
+            if xs[m, k] != 0.0:
+                out[m] += xs[m, k] * W[k]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CDNA4 tile layout (the engine's own repacked format; specified here so the
+# device repack can be checked bit for bit).
+#
+# Weights: tiles of 16 output columns x 128 input rows, 1 KiB each, tile
+# (nt, kt) at byte offset (nt * KT + kt) * 1024 with KT = ceil(K / 128).
+# Inside a tile, lane l (0..63) owns 16 bytes = 4 little-endian uint32 words;
+# word w holds column n = 16*nt + l % 16 and rows k0 .. k0+7 with
+# k0 = 128*kt + 32*w + 8*(l // 16); nibble p holds row k0 + AWQ_ORDER[p].
+# Out-of-range rows/columns hold 0.
+#
+# Scales: [NT][NG][16] in the scale dtype, NG = K // G (0 for padded columns).
+# Zeros:  [NT][NG] uint64, nibble c = zero point of column 16*nt + c.
+# The zeros array starts right after the scales array in one buffer.
+# ---------------------------------------------------------------------------
+
+TILE_N = 16
+TILE_K = 128
+
+
+def repacked_shapes(K: int, N: int, G: int) -> Dict[str, int]:
+    NT = -(-N // TILE_N)
+    KT = -(-K // TILE_K)
+    NG = K // G
+    return {"NT": NT, "KT": KT, "NG": NG,
+            "w_bytes": NT * KT * 1024,
+            "s_bytes": NT * NG * 16 * 2,
+            "z_bytes": NT * NG * 8}
+
+
+def repack_cdna4(qweight, qzeros, scales: torch.Tensor, group_size: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Return (weights uint8[w_bytes], scale_zero uint8[s_bytes + z_bytes])."""
+    q = unpack_awq(qweight)
+    z = unpack_awq(qzeros)
+    K, N = q.shape
+    G = resolve_group_size(group_size, K)
+    sh = repacked_shapes(K, N, G)
+    NT, KT, NG = sh["NT"], sh["KT"], sh["NG"]
+    qp = np.zeros((KT * TILE_K, NT * TILE_N), dtype=np.uint32)
+    qp[:K, :N] = q
+    # qp[kt, w, lg, j, nt, c] with k = 128 kt + 32 w + 8 lg + j, n = 16 nt + c
+    v = qp.reshape(KT, 4, 4, 8, NT, 16)
+    words = np.zeros((NT, KT, 4, 16, 4), dtype=np.uint32)  # [nt, kt, lg, c, w]
+    for p in range(8):
+        j = AWQ_ORDER[p]
+        # v[kt, w, lg, j, nt, c] at fixed j -> [nt, kt, lg, c, w]
+        words |= v[:, :, :, j, :, :].transpose(3, 0, 2, 4, 1) << np.uint32(4 * p)
+    wbuf = words.reshape(-1).view(np.uint8).copy()
+    assert wbuf.size == sh["w_bytes"]
+
+    s = scales.detach().cpu()
+    sp = torch.zeros((NG, NT * TILE_N), dtype=s.dtype)
+    sp[:, :N] = s
+    s_r = sp.reshape(NG, NT, 16).permute(1, 0, 2).contiguous()
+    sbytes = s_r.view(torch.int16).numpy().view(np.uint8).reshape(-1)
+    zp = np.zeros((NG, NT * TILE_N), dtype=np.uint64)
+    zp[:, :N] = z
+    zr = zp.reshape(NG, NT, 16).transpose(1, 0, 2)
+    zw = np.zeros((NT, NG), dtype=np.uint64)
+    for c in range(16):
+        zw |= zr[:, :, c] << np.uint64(4 * c)
+    zbytes = zw.reshape(-1).view(np.uint8)
+    return wbuf, np.concatenate([sbytes, zbytes])
+
+
+def unrepack_cdna4(wbuf: np.ndarray, szbuf: np.ndarray, K: int, N: int, group_size: int,
+                   dtype: torch.dtype) -> Tuple[np.ndarray, np.ndarray, torch.Tensor]:
+    """Inverse of :func:`repack_cdna4` (returns AWQ qweight, qzeros, scales)."""
+    G = resolve_group_size(group_size, K)
+    sh = repacked_shapes(K, N, G)
+    NT, KT, NG = sh["NT"], sh["KT"], sh["NG"]
+    words = np.ascontiguousarray(wbuf).view(np.uint32).reshape(NT, KT, 4, 16, 4)
+    v = np.zeros((KT, 4, 4, 8, NT, 16), dtype=np.uint32)
+    for p in range(8):
+        v[:, :, :, AWQ_ORDER[p], :, :] = ((words >> np.uint32(4 * p)) & np.uint32(0xF)).transpose(1, 4, 2, 0, 3)
+    q = v.reshape(KT * TILE_K, NT * TILE_N)[:K, :N]
+    sb = np.ascontiguousarray(szbuf[: sh["s_bytes"]]).view(np.int16)
+    s_r = torch.from_numpy(sb.copy()).view(dtype).reshape(NT, NG, 16)
+    scales = s_r.permute(1, 0, 2).reshape(NG, NT * TILE_N)[:, :N].contiguous()
+    zw = np.ascontiguousarray(szbuf[sh["s_bytes"]: sh["s_bytes"] + sh["z_bytes"]]).view(np.uint64).reshape(NT, NG)
+    z = np.zeros((NG, NT * 16), dtype=np.int32)
+    for c in range(16):
+        z[:, c::16] = ((zw >> np.uint64(4 * c)) & np.uint64(0xF)).astype(np.int32).T
+    return pack_awq(q), pack_awq(z[:, :N]), scales
+
+
+# ---------------------------------------------------------------------------
+# Fused MoE (config: experts stacked on dim 0, AWQ gate_up [E, H, 2I] and
+# down [E, I, H] in the AWQ orientation of a linear, i.e. qweight [E, K, N/8]).
+# ---------------------------------------------------------------------------
+
+def fused_topk(router_logits: torch.Tensor, topk: int, renormalize: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """softmax(fp32 logits) -> top-k -> optional renormalise (fused.py:11-31)."""
+    p = torch.softmax(router_logits.detach().cpu().float(), dim=-1)
+    w, ids = torch.topk(p, topk, dim=-1)
+    if renormalize:
+        w = w / (w.sum(dim=-1, keepdim=True) + 1e-8)
+    return w, ids.to(torch.int32)
+
+
+def silu_and_mul(h: torch.Tensor) -> torch.Tensor:
+    """silu(h[..., :d]) * h[..., d:] in fp32 (activation.py:11-15: gate half first)."""
+    d = h.shape[-1] // 2
+    hf = h.float()
+    return torch.nn.functional.silu(hf[..., :d]) * hf[..., d:]
+
+
+def fused_moe_awq(x: torch.Tensor, w1: Dict[str, torch.Tensor], w2: Dict[str, torch.Tensor],
+                  topk_weights: torch.Tensor, topk_ids: torch.Tensor, group_size: int) -> torch.Tensor:
+    """Grouped AWQ MoE following fused.py:101-202 and triton/fused_moe.py:7-50, 174-178.
+
+    GEMM1 per (token, slot) in fp32, cast to the activation dtype; silu_and_mul
+    (computed in fp32, cast); GEMM2 in fp32 times the routed weight (fp32)
+    before the cast; the top-k outputs are summed in fp32 and cast.
+    ``w1``/``w2`` hold expert-stacked ``qweight``/``qzeros``/``scales``.
+    """
+    dt = x.dtype
+    T, H = x.shape
+    E = w1["qweight"].shape[0]
+    k = topk_ids.shape[1]
+    W1 = [dequantize(w1["qweight"][e], w1["qzeros"][e], w1["scales"][e], group_size).float() for e in range(E)]
+    W2 = [dequantize(w2["qweight"][e], w2["qzeros"][e], w2["scales"][e], group_size).float() for e in range(E)]
+    xf = x.detach().cpu().float()
+    out = torch.zeros((T, W2[0].shape[1]), dtype=torch.float32)
+    ids = topk_ids.cpu().long()
+    tw = topk_weights.cpu().float()
+    for e in range(E):
+        rows, slots = torch.nonzero(ids == e, as_tuple=True)
+        if rows.numel() == 0:
+            continue
+        h1 = (xf[rows] @ W1[e]).to(dt)
+        h2 = silu_and_mul(h1).to(dt)
+        y = (h2.float() @ W2[e]) * tw[rows, slots][:, None]
+        out.index_put_((rows,), y.to(dt).float(), accumulate=True)
+    return out.to(dt)
+
+
+def fused_moe_awq_loops(x, w1, w2, topk_weights, topk_ids, group_size) -> torch.Tensor:
+    """Explicit per-(token, slot) loop form of :func:`fused_moe_awq` (tiny shapes only)."""
+    dt = x.dtype
+    T, H = x.shape
+    k = topk_ids.shape[1]
+    out = []
+    for t in range(T):
+        acc = None
+        for j in range(k):
+            e = int(topk_ids[t, j])
+            W1 = dequantize(w1["qweight"][e], w1["qzeros"][e], w1["scales"][e], group_size).float()
+            W2 = dequantize(w2["qweight"][e], w2["qzeros"][e], w2["scales"][e], group_size).float()
+            h1 = (x[t].float() @ W1).to(dt)
+            d = h1.shape[0] // 2
+            g = h1[:d].float()
+            h2 = (g / (1.0 + torch.exp(-g)) * h1[d:].float()).to(dt)
+            y = ((h2.float() @ W2) * float(topk_weights[t, j])).to(dt).float()
+            acc = y if acc is None else acc + y
+        out.append(acc)
+    return torch.stack(out).to(dt)
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs (weights/scales/activations as the workloads state).
+# ---------------------------------------------------------------------------
+
+def make_awq_linear(K: int, N: int, group_size: int = 128, seed: int = 0,
+                    dtype: torch.dtype = torch.float16) -> Dict[str, torch.Tensor]:
+    """Nibbles uniform 0..15, scales uniform [0.002, 0.02], drawn in this order:
+    q [K, N], z [K/G, N], s [K/G, N] from one torch.Generator seeded with ``seed``."""
+    G = resolve_group_size(group_size, K)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(0, 16, (K, N), generator=g, dtype=torch.int32)
+    z = torch.randint(0, 16, (K // G, N), generator=g, dtype=torch.int32)
+    s = (torch.rand((K // G, N), generator=g) * 0.018 + 0.002).to(dtype)
+    return {"qweight": torch.from_numpy(pack_awq(q)), "qzeros": torch.from_numpy(pack_awq(z)), "scales": s}
+
+
+def make_activation(M: int, K: int, seed: int, dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn((M, K), generator=g).to(dtype)
+
+
+def tolerance_ok(out: torch.Tensor, ref: torch.Tensor, rel: float = 2e-2) -> Tuple[bool, float, float]:
+    """The GEMM contract: max|out - ref| <= rel * max|ref|."""
+    o = out.detach().cpu().float()
+    r = ref.detach().cpu().float()
+    err = float((o - r).abs().max()) if o.numel() else 0.0
+    mx = float(r.abs().max()) if r.numel() else 0.0
+    return err <= rel * mx or (mx == 0.0 and err == 0.0), err, mx
+
+
+def bf16_round_bits(x64: np.ndarray) -> np.ndarray:
+    """Round float64 values (exactly representable in fp32) to bf16 bit patterns
+    by integer round-to-nearest-even on the fp32 encoding (independent of torch)."""
+    f = x64.astype(np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (f >> np.uint64(16)) & np.uint64(1)
+    r = (f + np.uint64(0x7FFF) + lsb) >> np.uint64(16)
+    return r.astype(np.uint16)
+
+
+def gemm_bytes(M: int, N: int, K: int, G: int = 128, act_bytes: int = 2) -> int:
+    """Algorithmic HBM bytes of one linear: int4 weights, packed zeros, scales, x, y."""
+    return K * N // 2 + (K // G) * N // 2 + (K // G) * N * 2 + act_bytes * M * K + act_bytes * M * N
+
+
+def gemm_flops(M: int, N: int, K: int) -> int:
+    return 2 * M * N * K
+
+
+__all__ = [name for name in dir() if not name.startswith("_") and name not in ("annotations", "math", "np", "torch")]

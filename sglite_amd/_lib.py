@@ -1,0 +1,90 @@
+"""ctypes binding of libsglite_awq.so (the C ABI in include/sglite_awq.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``make -C sglite_amd/csrc``).  There is no fallback: if the library is missing
+every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsglite_awq.so")
+
+AWQ_STATUS_OK = 0
+AWQ_STATUS_INVALID_ARGUMENT = -1
+AWQ_STATUS_UNSUPPORTED = -2
+AWQ_STATUS_HIP_ERROR = -3
+AWQ_STATUS_WORKSPACE = -4
+
+AWQ_DTYPE_FP16 = 0
+AWQ_DTYPE_BF16 = 1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES = {
+    "awq_last_error": (ctypes.c_char_p, []),
+    "awq_version": (ctypes.c_char_p, []),
+    "awq_repacked_weight_bytes": (_i64, [_i64, _i64]),
+    "awq_repacked_scale_bytes": (_i64, [_i64, _i64, _i64]),
+    "awq_repacked_zero_bytes": (_i64, [_i64, _i64, _i64]),
+    "awq_repack_cdna4": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "awq_unrepack_cdna4": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "awq_dequant": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "awq_dequant_repacked": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "awq_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "awq_counter_bytes": (_i64, [_i64]),
+    "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class AWQKernelError(RuntimeError):
+    """A HIP-side failure reported by the C ABI."""
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: the AWQ HIP engine is not built "
+            "(run __graft_entry__.build() or `make -C sglite_amd/csrc`)."
+        )
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().awq_last_error().decode()
+
+
+def check(status: int, what: str) -> int:
+    """Map a C-ABI status to the reference's exception types.
+
+    Shape/config problems raise ValueError, as the reference's linear methods
+    do (python/sglite/srt/model_executor/layers/quantization/awq.py:76-85);
+    everything else raises RuntimeError.
+    """
+    if status >= 0:
+        return status
+    msg = f"{what}: {last_error()}"
+    if status == AWQ_STATUS_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    if status == AWQ_STATUS_HIP_ERROR:
+        raise AWQKernelError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,198 @@
+// C ABI of the AWQ W4A16 engine (declared in include/sglite_awq.h).
+//
+// Argument validation mirrors the reference's checks and turns each into a
+// status code plus a thread-local message instead of a Python exception:
+//   group size in {-1, 32, 64, 128} or == K
+//     (layers/quantization/awq_triton.py:159-166, marlin_utils.py:86-88)
+//   K % G == 0, N % 8 == 0 (layers/quantization/awq.py:76-85)
+// The Python wrapper raises ValueError for AWQ_STATUS_INVALID_ARGUMENT and
+// RuntimeError otherwise.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/sglite_awq.h"
+#include "awq_launch.h"
+
+using namespace sgl_awq;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return AWQ_STATUS_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Shape rules shared by every entry point.  On success *G_out holds the
+// resolved group size.
+int check_shape(int64_t K, int64_t N, int64_t G, int dtype, int64_t* G_out) {
+  if (dtype != AWQ_DTYPE_FP16 && dtype != AWQ_DTYPE_BF16)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "dtype must be AWQ_DTYPE_FP16 (0) or AWQ_DTYPE_BF16 (1), got %d", dtype);
+  if (K <= 0 || N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "K and N must be positive (K=%lld, N=%lld)",
+                                    (long long)K, (long long)N);
+  if (K > (int64_t(1) << 30) || N > (int64_t(1) << 30))
+    return fail(AWQ_STATUS_UNSUPPORTED, "K and N must be below 2^30 (K=%lld, N=%lld)", (long long)K, (long long)N);
+  const int64_t Gr = (G == -1) ? K : G;
+  if (!(Gr == 32 || Gr == 64 || Gr == 128 || Gr == K))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "group size must be -1, 32, 64, 128 or K, got %lld", (long long)G);
+  if (K % Gr != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "The input size is not aligned with the quantized weight shape (K=%lld, group size %lld).",
+                (long long)K, (long long)Gr);
+  if (K % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "K must be a multiple of 32, got %lld", (long long)K);
+  if (N % 8 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "The output size is not aligned with the quantized weight shape (N=%lld, pack factor 8).",
+                (long long)N);
+  *G_out = Gr;
+  return AWQ_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* awq_last_error(void) { return g_last_error.c_str(); }
+
+const char* awq_version(void) { return "sglite-awq-gfx950 0.1"; }
+
+int64_t awq_repacked_weight_bytes(int64_t K, int64_t N) {
+  if (K <= 0 || N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "K and N must be positive");
+  return ((N + 15) / 16) * ((K + 127) / 128) * 1024;
+}
+
+int64_t awq_repacked_scale_bytes(int64_t K, int64_t N, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  return ((N + 15) / 16) * (K / Gr) * 16 * 2;
+}
+
+int64_t awq_repacked_zero_bytes(int64_t K, int64_t N, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  return ((N + 15) / 16) * (K / Gr) * 8;
+}
+
+int awq_repack_cdna4(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype, int64_t K,
+                     int64_t N, int64_t G, void* w_out, void* s_out, void* z_out, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (!qweight || !qzeros || !scales || !w_out || !s_out || !z_out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_repack_cdna4: null pointer argument");
+  if (!aligned(w_out, 16) || !aligned(s_out, 16) || !aligned(z_out, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_repack_cdna4: output buffers must be 16-byte aligned");
+  const Geom g = make_geom(0, N, K, Gr);
+  return hip_status(launch_repack(qweight, qzeros, scales, dtype, g, w_out, s_out, z_out, (hipStream_t)stream),
+                    "awq_repack_cdna4 launch");
+}
+
+int awq_unrepack_cdna4(const void* w, const void* s, const void* z, int dtype, int64_t K, int64_t N, int64_t G,
+                       int32_t* qweight_out, int32_t* qzeros_out, void* scales_out, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (!w || !s || !z || !qweight_out || !qzeros_out || !scales_out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_unrepack_cdna4: null pointer argument");
+  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_unrepack_cdna4: repacked buffers must be 16-byte aligned");
+  const Geom g = make_geom(0, N, K, Gr);
+  return hip_status(
+      launch_unrepack(w, s, z, dtype, g, qweight_out, qzeros_out, scales_out, (hipStream_t)stream),
+      "awq_unrepack_cdna4 launch");
+}
+
+int awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype, int64_t K, int64_t N,
+                int64_t G, void* w_out, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (!qweight || !qzeros || !scales || !w_out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_dequant: null pointer argument");
+  const Geom g = make_geom(0, N, K, Gr);
+  return hip_status(launch_dequant_awq(qweight, qzeros, scales, dtype, g, w_out, (hipStream_t)stream),
+                    "awq_dequant launch");
+}
+
+int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype, int64_t K, int64_t N, int64_t G,
+                         void* w_out, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (!w || !s || !z || !w_out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_dequant_repacked: null pointer argument");
+  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_dequant_repacked: repacked buffers must be 16-byte aligned");
+  const Geom g = make_geom(0, N, K, Gr);
+  return hip_status(launch_dequant_repacked(w, s, z, dtype, g, w_out, (hipStream_t)stream),
+                    "awq_dequant_repacked launch");
+}
+
+int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative");
+  if (M == 0) return 0;
+  return plan_gemm(make_geom(M, N, K, Gr)).ws_bytes;
+}
+
+int64_t awq_counter_bytes(int64_t N) {
+  if (N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "N must be positive");
+  return ((N + 15) / 16) * 4;
+}
+
+int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
+                   int64_t M, int64_t N, int64_t K, int64_t G, int dtype, void* ws, int64_t ws_bytes,
+                   int32_t* counters, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative, got %lld", (long long)M);
+  if (M == 0) return ok();
+  if (M > (int64_t(1) << 24)) return fail(AWQ_STATUS_UNSUPPORTED, "M must be below 2^24, got %lld", (long long)M);
+  if (!x || !w || !s || !z || !out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: null pointer argument");
+  if (!aligned(x, 16)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: x must be 16-byte aligned");
+  if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: out must be 8-byte aligned");
+  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: repacked buffers must be 16-byte aligned");
+  if (bias && !aligned(bias, 2))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: bias must be 2-byte aligned");
+  const Geom g = make_geom(M, N, K, Gr);
+  const GemmPlan p = plan_gemm(g);
+  if (p.ws_bytes > 0) {
+    if (!ws || ws_bytes < p.ws_bytes)
+      return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: workspace of %lld bytes needed, %lld given",
+                  (long long)p.ws_bytes, (long long)(ws ? ws_bytes : 0));
+    if (!aligned(ws, 16)) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: workspace must be 16-byte aligned");
+    if (!counters) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: split-K needs the counters buffer");
+  }
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, (hipStream_t)stream),
+                    "awq_w4a16_gemm launch");
+}
+
+}  // extern "C"

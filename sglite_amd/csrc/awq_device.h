@@ -1,0 +1,134 @@
+// Device helpers shared by the AWQ W4A16 kernels (gfx950 / CDNA4, wave64).
+//
+// Repacked tile layout (the "CDNA4 tile layout"):
+//   weights: 1 KiB tiles of 16 columns x 128 rows; tile (nt, kt) at
+//            (nt * KT + kt) KiB.  Lane l of a tile owns one 16-byte vector
+//            (4 uint32 words); word w holds column 16*nt + (l & 15) and rows
+//            k0..k0+7, k0 = 128*kt + 32*w + 8*(l >> 4); nibble p holds row
+//            k0 + {0,2,4,6,1,3,5,7}[p].
+//   So one 16-byte load per lane is exactly the MFMA 16x16x32 operand of four
+//   consecutive 32-row k-blocks for that lane's column, and the nibble order
+//   lets (word >> 4i) & 0x000F000F produce the packed pair (row 2i, row 2i+1).
+//   scales:  [NT][NG][16] in the activation dtype.
+//   zeros:   [NT][NG] uint64, nibble c = zero point of column 16*nt + c.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sgl_awq {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTileN = 16;
+constexpr int kTileK = 128;
+constexpr int kTileWords = 256;  // 1 KiB
+
+// Activation / scale element type tags.
+struct F16 {
+  using elem = _Float16;
+  using vec8 = f16x8;
+  using vec4 = f16x4;
+};
+struct BF16 {
+  using elem = __bf16;
+  using vec8 = bf16x8;
+  using vec4 = bf16x4;
+};
+
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Group-dependent dequantisation constants of one lane's column.
+struct ZS16 {
+  f16x2 zb;  // (1024 + z) twice
+  f16x2 s;   // scale twice
+};
+struct ZSbf {
+  float z;
+  float s;
+};
+
+template <typename DT>
+struct Dq;
+
+// fp16: (w >> 4i) & 0x000F000F | 0x6400 6400 is the fp16 pair (1024 + q_lo,
+// 1024 + q_hi) exactly; subtracting (1024 + z) is exact (integers below 2048),
+// and the one packed multiply by the scale is the single round-to-nearest-even
+// of (q - z) * s that the oracle specifies.
+template <>
+struct Dq<F16> {
+  using ZS = ZS16;
+  __device__ __forceinline__ static ZS make(uint32_t z, uint16_t sbits) {
+    ZS r;
+    uint32_t zb = 0x6400u | z;
+    r.zb = __builtin_bit_cast(f16x2, zb | (zb << 16));
+    r.s = __builtin_bit_cast(f16x2, (uint32_t)sbits | ((uint32_t)sbits << 16));
+    return r;
+  }
+  __device__ __forceinline__ static f16x8 word(uint32_t w, const ZS& zs) {
+    const uint32_t a0 = (w & 0x000F000Fu) | 0x64006400u;
+    const uint32_t a1 = ((w >> 4) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t a2 = ((w >> 8) & 0x000F000Fu) | 0x64006400u;
+    const uint32_t a3 = ((w >> 12) & 0x000F000Fu) | 0x64006400u;
+    f16x2 h0 = (__builtin_bit_cast(f16x2, a0) - zs.zb) * zs.s;
+    f16x2 h1 = (__builtin_bit_cast(f16x2, a1) - zs.zb) * zs.s;
+    f16x2 h2 = (__builtin_bit_cast(f16x2, a2) - zs.zb) * zs.s;
+    f16x2 h3 = (__builtin_bit_cast(f16x2, a3) - zs.zb) * zs.s;
+    f16x8 r;
+    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+    return r;
+  }
+};
+
+// bf16: (q - z) * s is exact in fp32 (4-bit by 8-bit significands) and the
+// conversion to bf16 is the single round-to-nearest-even.
+template <>
+struct Dq<BF16> {
+  using ZS = ZSbf;
+  __device__ __forceinline__ static ZS make(uint32_t z, uint16_t sbits) {
+    ZS r;
+    r.z = (float)z;
+    r.s = __builtin_bit_cast(float, (uint32_t)sbits << 16);
+    return r;
+  }
+  __device__ __forceinline__ static bf16x8 word(uint32_t w, const ZS& zs) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = (float)((w >> (4 * i)) & 0xFu);
+      const float hi = (float)((w >> (4 * i + 16)) & 0xFu);
+      r[2 * i] = (__bf16)((lo - zs.z) * zs.s);
+      r[2 * i + 1] = (__bf16)((hi - zs.z) * zs.s);
+    }
+    return r;
+  }
+};
+
+__device__ __forceinline__ uint32_t zero_nibble(uint64_t zw, int c) {
+  return (uint32_t)(zw >> (4 * c)) & 0xFu;
+}
+
+// Round an fp32 accumulator to the output dtype, then add the bias in that
+// dtype (the reference adds bias to the already-rounded GEMM output,
+// awq.py:145-146 / marlin_utils.py:412-413).
+template <typename DT>
+__device__ __forceinline__ typename DT::elem finish(float acc, const typename DT::elem* bias, int n) {
+  typename DT::elem r = (typename DT::elem)acc;
+  if (bias != nullptr) r = (typename DT::elem)((float)r + (float)bias[n]);
+  return r;
+}
+
+}  // namespace sgl_awq

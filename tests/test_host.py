@@ -1,0 +1,300 @@
+"""CPU tests of the host side: the C ABI library loads and exports every
+declared symbol, argument validation maps to the reference's exception types,
+and the plugin API (configs, linear methods, linear plumbing, config
+detection) behaves like python/sglite/srt/model_executor/layers/quantization/*
+and models/config.py.  No test here launches GPU work."""
+
+import ctypes
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as oracle
+from sglite_amd import _lib
+from sglite_amd.quantization import (LinearMethodBase, QuantizationConfig, UnquantizedLinearMethod,
+                                     get_quantization_config, set_weight_attrs)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sglite_awq.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(awq_[a-z0-9_]+)\s*\(", text)))
+
+
+# --------------------------------------------------------------------------
+# C ABI
+# --------------------------------------------------------------------------
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, name
+    assert set(_lib.SIGNATURES) == set(declared)
+
+
+def test_version_and_empty_error():
+    lib = _lib.load()
+    assert lib.awq_version().decode().startswith("sglite-awq-gfx950")
+
+
+@pytest.mark.parametrize("K,N,G", [(2560, 6144, 128), (96, 24, 32), (384, 40, -1), (4096, 28672, 64)])
+def test_size_queries_match_layout(K, N, G):
+    lib = _lib.load()
+    Gr = K if G == -1 else G
+    sh = oracle.repacked_shapes(K, N, Gr)
+    assert lib.awq_repacked_weight_bytes(K, N) == sh["w_bytes"]
+    assert lib.awq_repacked_scale_bytes(K, N, G) == sh["s_bytes"]
+    assert lib.awq_repacked_zero_bytes(K, N, G) == sh["z_bytes"]
+    assert lib.awq_counter_bytes(N) == 4 * ((N + 15) // 16)
+    assert lib.awq_workspace_bytes(0, N, K, G) == 0
+
+
+def test_workspace_query_is_bounded():
+    lib = _lib.load()
+    for (K, N) in [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)]:
+        for M in (1, 8, 32):
+            ws = lib.awq_workspace_bytes(M, N, K, 128)
+            assert ws >= 0
+            assert ws % (4 * M * 16) == 0
+            # split-K partials stay well below the int4 weight stream
+            assert ws <= K * N // 2
+        assert lib.awq_workspace_bytes(2048, N, K, 128) == 0  # tiled kernel needs no scratch
+
+
+@pytest.mark.parametrize("K,N,G,dtype,msg", [
+    (100, 64, 128, 0, "group size"),
+    (256, 64, 48, 0, "group size"),
+    (256, 60, 128, 0, "output size"),
+    (0, 64, 128, 0, "positive"),
+    (256, 64, 128, 7, "dtype"),
+    (96, 64, 64, 0, "input size"),
+])
+def test_invalid_shapes_raise_value_error(K, N, G, dtype, msg):
+    lib = _lib.load()
+    fake = 0x10000  # never dereferenced: validation fails first
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 4, N, K, G, dtype, None, 0, None, None)
+    assert st == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    with pytest.raises(ValueError, match=msg):
+        _lib.check(st, "awq_w4a16_gemm")
+
+
+def test_null_and_misaligned_pointers_rejected():
+    lib = _lib.load()
+    fake = 0x10000
+    assert lib.awq_w4a16_gemm(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, None) == -1
+    assert "null" in _lib.last_error()
+    assert lib.awq_w4a16_gemm(fake + 2, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, None) == -1
+    assert "aligned" in _lib.last_error()
+    assert lib.awq_repack_cdna4(fake, fake, fake, 0, 256, 64, 128, fake + 4, fake, fake, None) == -1
+    assert lib.awq_dequant(None, fake, fake, 0, 256, 64, 128, fake, None) == -1
+
+
+def test_missing_workspace_is_reported_before_launch():
+    lib = _lib.load()
+    fake = 0x10000
+    K, N, M = 4096, 2560, 1
+    need = lib.awq_workspace_bytes(M, N, K, 128)
+    assert need > 0
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, None, 0, None, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.check(st, "awq_w4a16_gemm")
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, None, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE and "counters" in _lib.last_error()
+
+
+def test_m_zero_is_a_noop():
+    # an empty batch launches nothing, so no buffer is needed (shape checks still apply)
+    lib = _lib.load()
+    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 64, 256, 128, 0, None, 0, None, None) == 0
+    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 60, 256, 128, 0, None, 0, None, None) == -1
+    fake = 0x10000
+    assert lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 0, 64, 256, 128, 0, None, 0, None, None) == 0
+
+
+# --------------------------------------------------------------------------
+# configs and methods (quantization/__init__.py, base_config.py, awq.py, awq_marlin.py)
+# --------------------------------------------------------------------------
+
+def test_get_quantization_config_names():
+    from sglite_amd.quantization.awq import AWQConfig
+    from sglite_amd.quantization.awq_marlin import AWQMarlinConfig
+
+    assert get_quantization_config("AWQ") is AWQConfig
+    assert get_quantization_config("awq_marlin") is AWQMarlinConfig
+    with pytest.raises(ValueError, match="Unknown quantization method"):
+        get_quantization_config("gptq")
+
+
+def test_lazy_exports():
+    import sglite_amd.quantization as q
+
+    assert q.AWQLinearMethod.__name__ == "AWQLinearMethod"
+    assert q.AWQMarlinLinearMethod.__name__ == "AWQMarlinLinearMethod"
+    with pytest.raises(AttributeError):
+        q.NotAThing  # noqa: B018
+
+
+def test_awq_config_from_config_and_errors():
+    cls = get_quantization_config("awq")
+    cfg = cls.from_config({"w_bit": 4, "q_group_size": 128, "zero_point": True})
+    assert (cfg.weight_bits, cfg.group_size, cfg.zero_point, cfg.pack_factor) == (4, 128, True, 8)
+    assert cfg.get_name() == "awq"
+    assert cfg.get_supported_act_dtypes() == [torch.half]
+    assert cfg.get_config_filenames() == ["quant_config.json", "quantize_config.json"]
+    assert isinstance(cfg.get_linear_method(), LinearMethodBase)
+    with pytest.raises(ValueError, match="only 4-bit"):
+        cls(8, 128, True)
+    with pytest.raises(ValueError, match="Cannot find any of"):
+        cls.from_config({"bits": 4, "zero_point": True})
+    assert QuantizationConfig.get_from_keys({"bits": 4, "w_bit": 8}, ["w_bit", "bits"]) == 8
+
+
+def test_awq_marlin_config_rules():
+    cls = get_quantization_config("awq_marlin")
+    cfg = cls.from_config({"bits": 4, "group_size": 64, "zero_point": True})
+    assert cfg.quant_type.size_bits == 4 and cfg.get_name() == "awq_marlin"
+    assert cfg.get_supported_act_dtypes() == [torch.half, torch.bfloat16]
+    with pytest.raises(ValueError, match="does not support this configuration"):
+        cls(8, 128, True)  # uint8 with zero points is not served (marlin_utils.py:91-96)
+    with pytest.raises(ValueError, match="does not support this configuration"):
+        cls(4, 256, True)
+    with pytest.raises(ValueError, match="only supports"):
+        cls(3, 128, True)
+    ok = {"quant_method": "awq", "bits": 4, "group_size": 128, "zero_point": True}
+    assert cls.is_awq_marlin_compatible(ok)
+    assert not cls.is_awq_marlin_compatible({**ok, "quant_method": "gptq"})
+    assert not cls.is_awq_marlin_compatible({**ok, "bits": 8})
+    assert not cls.is_awq_marlin_compatible({k: v for k, v in ok.items() if k != "zero_point"})
+    assert not cls.is_awq_marlin_compatible({**ok, "group_size": 96})
+    assert cls.is_awq_marlin_compatible({**ok, "group_size": -1})
+
+
+def test_set_weight_attrs_refuses_overwrite():
+    t = torch.empty(2)
+    set_weight_attrs(t, {"input_dim": 0})
+    set_weight_attrs(t, None)
+    with pytest.raises(RuntimeError, match="Overwriting"):
+        set_weight_attrs(t, {"input_dim": 1})
+
+
+def test_awq_create_weights_shapes_and_errors():
+    m = get_quantization_config("awq")(4, 128, True).get_linear_method()
+    w = m.create_weights(2560, 6144)
+    assert w["qweight"].shape == (2560, 768) and w["qweight"].dtype == torch.int32
+    assert w["qzeros"].shape == (20, 768) and w["qzeros"].dtype == torch.int32
+    assert w["scales"].shape == (20, 6144) and w["scales"].dtype == torch.get_default_dtype()
+    assert (w["qweight"].packed_dim, w["qweight"].pack_factor, w["scales"].output_dim) == (1, 8, 1)
+    assert set(w) == {"qweight", "qzeros", "scales"}
+    with pytest.raises(ValueError, match="input size is not aligned"):
+        m.create_weights(2500, 6144)
+    with pytest.raises(ValueError, match="output size is not aligned"):
+        m.create_weights(2560, 6140)
+
+
+def test_awq_marlin_create_weights_metadata_and_errors():
+    m = get_quantization_config("awq_marlin")(4, -1, True).get_linear_method()
+    w = m.create_weights(256, 128)
+    assert w["qzeros"].shape == (1, 16) and w["_num_groups"] == 1
+    assert (w["_input_size"], w["_output_size"], w["_weights_processed"]) == (256, 128, False)
+    m = get_quantization_config("awq_marlin")(4, 128, True).get_linear_method()
+    with pytest.raises(ValueError, match="not divisible by 64"):
+        m.create_weights(256, 96)
+    with pytest.raises(ValueError, match="not divisible by 128"):
+        m.create_weights(192, 128)
+
+
+def test_scale_dtype_follows_default_dtype():
+    m = get_quantization_config("awq")(4, 128, True).get_linear_method()
+    old = torch.get_default_dtype()
+    try:
+        torch.set_default_dtype(torch.bfloat16)
+        assert m.create_weights(256, 64)["scales"].dtype == torch.bfloat16
+    finally:
+        torch.set_default_dtype(old)
+
+
+# --------------------------------------------------------------------------
+# linear plumbing (linear.py) with the dense method, on CPU
+# --------------------------------------------------------------------------
+
+def test_linear_plumbing_dense_roundtrip():
+    from sglite_amd.linear import MergedColumnParallelLinear, QKVParallelLinear, RowParallelLinear
+
+    lin = MergedColumnParallelLinear(32, [16, 16], has_bias=True)
+    assert lin.state_dict_keys("mlp.gate_up_proj") == ["mlp.gate_up_proj.weight", "mlp.gate_up_proj.bias"]
+    W = torch.randn(32, 32)
+    b = torch.randn(32)
+    sd = {"mlp.gate_up_proj.weight": W, "mlp.gate_up_proj.bias": b, "extra": torch.zeros(1)}
+    with pytest.raises(RuntimeError, match="Unexpected keys"):
+        lin.load_state_dict(dict(sd), prefix="mlp.gate_up_proj")
+    lin = MergedColumnParallelLinear(32, [16, 16], has_bias=True)
+    lin.load_state_dict({k: v for k, v in sd.items() if k != "extra"}, prefix="mlp.gate_up_proj")
+    x = torch.randn(3, 32)
+    torch.testing.assert_close(lin(x), x @ W.T + b)
+    qkv = QKVParallelLinear(64, 16, 4, 2, has_bias=False, tp_size=2)
+    assert qkv.local_output_size == (2 + 2 * 1) * 16
+    row = RowParallelLinear(64, 32, has_bias=False, tp_size=2)
+    assert row.local_input_size == 32
+    with pytest.raises(AssertionError):
+        RowParallelLinear(64, 32, has_bias=False).load_state_dict({"weight": torch.randn(32, 63)})
+
+
+def test_linear_plumbing_processes_once_and_hides_runtime_tensors():
+    from sglite_amd.linear import ReplicatedLinear
+
+    calls = []
+
+    class Probe(UnquantizedLinearMethod):
+        def create_weights(self, i, o):
+            w = super().create_weights(i, o)
+            w["_meta"] = 7
+            return w
+
+        def process_weights_after_loading(self, weights):
+            calls.append(dict(weights))
+            return {"weight": weights["weight"] * 2, "workspace": torch.zeros(3), "_meta": weights["_meta"]}
+
+    lin = ReplicatedLinear(8, 4, has_bias=False, linear_method=Probe())
+    assert lin.state_dict_keys() == ["weight"]
+    W = torch.randn(4, 8)
+    lin.load_state_dict({"weight": W})
+    assert len(calls) == 1 and calls[0]["_meta"] == 7
+    assert lin.state_dict_keys() == ["weight"]  # workspace did not become an attribute
+    assert "workspace" in lin._weights and lin._weights["_meta"] == 7
+    torch.testing.assert_close(lin.weight, W * 2)
+
+
+# --------------------------------------------------------------------------
+# quant-config detection (models/config.py:28-89)
+# --------------------------------------------------------------------------
+
+def test_load_quantization_config_sources(tmp_path):
+    from sglite_amd.model_config import load_quantization_config
+    from sglite_amd.quantization.awq import AWQConfig
+    from sglite_amd.quantization.awq_marlin import AWQMarlinConfig
+
+    class HF:
+        quantization_config = {"quant_method": "awq", "bits": 4, "group_size": 128, "zero_point": True}
+
+    assert isinstance(load_quantization_config("nowhere", HF()), AWQMarlinConfig)
+    assert isinstance(load_quantization_config("nowhere", HF(), force_awq_triton=True), AWQConfig)
+    (tmp_path / "quant_config.json").write_text(json.dumps({"w_bit": 4, "q_group_size": 64, "zero_point": True}))
+    cfg = load_quantization_config(str(tmp_path))
+    assert isinstance(cfg, AWQConfig) and cfg.group_size == 64  # no quant_method -> not Marlin-compatible
+    assert load_quantization_config(str(tmp_path / "missing")) is None
+
+    class GPTQ:
+        quantization_config = {"quant_method": "gptq", "bits": 4}
+
+    assert load_quantization_config("nowhere", GPTQ()) is None
