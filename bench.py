@@ -1,0 +1,268 @@
+#!/usr/bin/env python
+"""AWQ W4A16 GEMM throughput on one MI355X.
+
+Workload (decode regime, HBM-bound): one Qwen3-4B decoder layer's four AWQ
+linears -- qkv 2560->6144, o_proj 4096->2560, gate_up 2560->19456,
+down 9728->2560 -- int4 with group-128 zero points and fp16 scales (nibbles
+uniform 0..15, scales uniform [0.002, 0.02]), fp16 activations ~N(0,1) at
+M = 1, 8 and 32.  One step runs the four linears at each of the three M
+values (12 GEMMs) on one of 36 distinct weight copies (1.9 GB in total, far
+past the 256 MB Infinity Cache), rotating copies from step to step; each step
+is one HIP-graph replay, as decode steps are replayed in SGLite.
+
+value = algorithmic bytes of the timed steps / their time (GB/s), where one
+linear moves K*N/2 (int4) + (K/128)*N/2 (zeros) + (K/128)*N*2 (scales)
++ 2*M*K (x) + 2*M*N (y) bytes.
+
+Also reported on the same line:
+  roofline      the decode kernel (skinny_kernel, every GEMM of the step): per
+                launch algorithmic bytes / average launch duration, measured
+                with HIP events around graphs of back-to-back launches on the
+                launch stream, against 8 TB/s HBM.
+  per_m         the same per batch size.
+  prefill       Llama-3-8B's four linears at M = 2048, TFLOP/s against the
+                2.5 PFLOP/s dense fp16 MFMA peak (MFMA-bound regime).
+  cpu_baseline  the CPU oracle (dequantise + fp32 matmul + cast) on the host
+                cores for one pass of the layer at M = 1, 8, 32.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "AWQ W4A16 GEMM GB/s (M≤32) & TFLOP/s (M≥2048) vs roofline, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+G = 128
+LAYER = [("qkv_proj", 2560, 6144), ("o_proj", 4096, 2560), ("gate_up_proj", 2560, 19456), ("down_proj", 9728, 2560)]
+PREFILL = [("qkv_proj", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up_proj", 4096, 28672), ("down_proj", 14336, 4096)]
+M_SET = (1, 8, 32)
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def gemm_bytes(M: int, N: int, K: int) -> int:
+    return K * N // 2 + (K // G) * N // 2 + (K // G) * N * 2 + 2 * M * K + 2 * M * N
+
+
+def pack_awq_gpu(q: torch.Tensor) -> torch.Tensor:
+    """Logical 4-bit [R, C] -> AWQ int32 [R, C/8] (nibble p holds column 8j + AWQ_ORDER[p])."""
+    q = q.view(q.shape[0], -1, 8)
+    w = torch.zeros(q.shape[:2], dtype=torch.int32, device=q.device)
+    for p, col in enumerate(AWQ_ORDER):
+        w |= q[:, :, col] << (4 * p)
+    return w
+
+
+def make_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device):
+    q = torch.randint(0, 16, (K, N), generator=gen, device=dev, dtype=torch.int32)
+    z = torch.randint(0, 16, (K // G, N), generator=gen, device=dev, dtype=torch.int32)
+    s = (torch.rand((K // G, N), generator=gen, device=dev) * 0.018 + 0.002).to(torch.float16)
+    r = ops.repack(pack_awq_gpu(q), pack_awq_gpu(z), s)
+    del q, z, s
+    return r
+
+
+def graph_of(fn) -> torch.cuda.CUDAGraph:
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def time_replays(graphs, n: int) -> float:
+    """ms for n replays cycling through graphs, HIP events on the current stream."""
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for i in range(n):
+        graphs[i % len(graphs)].replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
+def cpu_baseline() -> dict:
+    from oracle import awq_oracle as oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    total_b, total_t = 0, 0.0
+    warm = oracle.make_awq_linear(256, 256, G, seed=0)
+    oracle.awq_gemm(oracle.make_activation(1, 256, 0), warm["qweight"], warm["qzeros"], warm["scales"], None, G)
+    for i, (_, K, N) in enumerate(LAYER):
+        t = oracle.make_awq_linear(K, N, G, seed=i)
+        for M in M_SET:
+            x = oracle.make_activation(M, K, seed=100 + M)
+            t0 = time.perf_counter()
+            oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+            total_t += time.perf_counter() - t0
+            total_b += gemm_bytes(M, N, K)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": "CPU oracle (numpy unpack + dequantise, fp32 torch matmul, fp16 cast) over the same layer's "
+                      f"4 linears at M=1,8,32, one pass each ({total_t:.1f} s); host {model}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--copies", type=int, default=36, help="distinct weight copies rotated through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
+              "design, not a measured path", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X", file=sys.stderr)
+        return 2
+
+    from sglite_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    C = args.copies
+    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in LAYER} for _ in range(C)]
+    cnts = [{name: ops.make_counters(N, dev) for name, K, N in LAYER} for _ in range(C)]
+    xg = torch.Generator(device=dev).manual_seed(1)
+    xs = {(M, K): torch.randn((M, K), generator=xg, device=dev).to(torch.float16)
+          for M in M_SET for K in {k for _, k, _ in LAYER}}
+    outs = {(M, name): torch.empty((M, N), dtype=torch.float16, device=dev) for M in M_SET for name, _, N in LAYER}
+    torch.cuda.synchronize()
+
+    def linear(c, M, name, K, N):
+        ops.gemm(xs[(M, K)], reps[c][name], K, N, G, counters=cnts[c][name], out=outs[(M, name)])
+
+    def step_fn(c):
+        def f():
+            for M in M_SET:
+                for name, K, N in LAYER:
+                    linear(c, M, name, K, N)
+        return f
+
+    steps = [graph_of(step_fn(c)) for c in range(C)]
+    step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
+    time_replays(steps, args.warmup)
+    ms = time_replays(steps, args.steps)
+    ms_per_step = ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # Per-launch durations of the decode kernel: graphs of C back-to-back
+    # launches of one (M, linear) over the C weight copies.
+    per_m, kb, kt = {}, 0, 0.0
+    for M in M_SET:
+        mb, mt, lin = 0, 0.0, {}
+        for name, K, N in LAYER:
+            def f(M=M, name=name, K=K, N=N):
+                for c in range(C):
+                    linear(c, M, name, K, N)
+            g = graph_of(f)
+            time_replays([g], 2)
+            us = time_replays([g], 5) * 1e3 / (5 * C)
+            b = gemm_bytes(M, N, K)
+            lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1)}
+            mb += b
+            mt += us
+            del g
+        per_m[str(M)] = {"GB/s": round(mb / mt / 1e3, 1), "us_per_layer": round(mt, 3), "linears": lin}
+        kb += mb
+        kt += mt
+    achieved = kb / kt / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "skinny_kernel (decode split-K W4A16)",
+                "bytes_per_launch_avg": kb // (len(M_SET) * len(LAYER)),
+                "us_per_launch_avg": round(kt / (len(M_SET) * len(LAYER)), 3)}
+    del steps
+    torch.cuda.synchronize()
+
+    prefill = None
+    if not args.no_prefill:
+        M = 2048
+        x = {K: torch.randn((M, K), generator=xg, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
+        tot_f, tot_t, lin = 0, 0.0, {}
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for name, K, N in PREFILL:
+            r = make_repacked(ops, K, N, gen, dev)
+            cnt = ops.make_counters(N, dev)
+            out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            for _ in range(3):
+                ops.gemm(x[K], r, K, N, G, counters=cnt, out=out)
+            torch.cuda.synchronize()
+            n = 10
+            a.record()
+            for _ in range(n):
+                ops.gemm(x[K], r, K, N, G, counters=cnt, out=out)
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / n
+            fl = 2 * M * N * K
+            lin[name] = {"us": round(us, 1), "TFLOP/s": round(fl / us / 1e6, 1)}
+            tot_f += fl
+            tot_t += us
+            del r
+        tf = tot_f / tot_t / 1e6
+        prefill = {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, "
+                               "down 14336x4096) at M=2048, fp16", "TFLOP/s": round(tf, 1),
+                   "peak": MFMA_FP16_PEAK_TFLOPS, "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
+                   "kernel": "tiled_kernel", "linears": lin}
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "Qwen3-4B decoder layer AWQ linears (qkv 2560x6144, o_proj 4096x2560, "
+                               "gate_up 2560x19456, down 9728x2560), int4 group 128 with zero points, fp16 "
+                               "scales/activations, M in {1, 8, 32} per step, HIP-graph replay",
+                   "weight_copies": C, "weight_bytes_rotated": C * sum(gemm_bytes(0, N, K) for _, K, N in LAYER),
+                   "step_bytes": step_bytes},
+        "roofline": roofline,
+        "per_m": per_m,
+        "prefill": prefill,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -86,7 +86,7 @@ int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype,
 
 /* ---- W4A16 GEMM ------------------------------------------------------------
  * out[M, N] = rnd(x[M, K] @ W) (+ bias[N] in the activation dtype), fp32
- * accumulation.  Replaces awq_gemm_triton
+ * accumulation; bias (if any) must be 8-byte aligned.  Replaces awq_gemm_triton
  * (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:144-195,
  * called from awq.py:141-147) and gptq_marlin_gemm + bias
  * (python/sglite/srt/model_executor/layers/quantization/marlin_utils.py:388-415).

@@ -180,8 +180,8 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
   if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: out must be 8-byte aligned");
   if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
     return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: repacked buffers must be 16-byte aligned");
-  if (bias && !aligned(bias, 2))
-    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: bias must be 2-byte aligned");
+  if (bias && !aligned(bias, 8))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: bias must be 8-byte aligned");
   const Geom g = make_geom(M, N, K, Gr);
   const GemmPlan p = plan_gemm(g);
   if (p.ws_bytes > 0) {

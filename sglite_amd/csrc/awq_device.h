@@ -60,6 +60,32 @@ struct ZSbf {
   float s;
 };
 
+// (a & mask) | bits.  gfx9 VOP3 encodings (v_and_or_b32) take no literal
+// constants, so with literal masks the compiler emits v_and_b32 + v_or_b32.
+// Callers pass `mask`/`bits` through opaque_vgpr() once, outside the loops;
+// the compiler then selects one v_and_or_b32 itself (and, unlike inline asm
+// for the instruction, keeps tracking its hazards, e.g. before an MFMA reads
+// the result).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) { return (a & mask) | bits; }
+
+// The value v, hidden from constant folding and held in a VGPR.
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Typed load at a 32-bit byte offset from a uniform base pointer, so the
+// compiler can use the global_load saddr form (SGPR base + VGPR offset)
+// instead of per-lane 64-bit address arithmetic.
+template <typename T>
+__device__ __forceinline__ T ld_off(const void* base, uint32_t byte_off) {
+  return *(const T*)((const char*)base + byte_off);
+}
+template <typename T>
+__device__ __forceinline__ T ld_off_nt(const void* base, uint32_t byte_off) {
+  return __builtin_nontemporal_load((const T*)((const char*)base + byte_off));
+}
+
 template <typename DT>
 struct Dq;
 
@@ -78,18 +104,17 @@ struct Dq<F16> {
     return r;
   }
   __device__ __forceinline__ static f16x8 word(uint32_t w, const ZS& zs) {
-    const uint32_t a0 = (w & 0x000F000Fu) | 0x64006400u;
-    const uint32_t a1 = ((w >> 4) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t a2 = ((w >> 8) & 0x000F000Fu) | 0x64006400u;
-    const uint32_t a3 = ((w >> 12) & 0x000F000Fu) | 0x64006400u;
-    f16x2 h0 = (__builtin_bit_cast(f16x2, a0) - zs.zb) * zs.s;
-    f16x2 h1 = (__builtin_bit_cast(f16x2, a1) - zs.zb) * zs.s;
-    f16x2 h2 = (__builtin_bit_cast(f16x2, a2) - zs.zb) * zs.s;
-    f16x2 h3 = (__builtin_bit_cast(f16x2, a3) - zs.zb) * zs.s;
-    f16x8 r;
-    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
-    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
-    return r;
+    const uint32_t a0 = and_or(w, 0x000F000Fu, 0x64006400u);
+    const uint32_t a1 = and_or(w >> 4, 0x000F000Fu, 0x64006400u);
+    const uint32_t a2 = and_or(w >> 8, 0x000F000Fu, 0x64006400u);
+    const uint32_t a3 = and_or(w >> 12, 0x000F000Fu, 0x64006400u);
+    const f16x2 h0 = (__builtin_bit_cast(f16x2, a0) - zs.zb) * zs.s;
+    const f16x2 h1 = (__builtin_bit_cast(f16x2, a1) - zs.zb) * zs.s;
+    const f16x2 h2 = (__builtin_bit_cast(f16x2, a2) - zs.zb) * zs.s;
+    const f16x2 h3 = (__builtin_bit_cast(f16x2, a3) - zs.zb) * zs.s;
+    const u32x4 r = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                     __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3)};
+    return __builtin_bit_cast(f16x8, r);
   }
 };
 
@@ -116,6 +141,37 @@ struct Dq<BF16> {
     return r;
   }
 };
+
+// Biased operand: the fp16 pairs (1024 + q_lo, 1024 + q_hi) (bf16: 128 + q)
+// straight from the nibbles, with no zero subtraction or scaling.  The GEMM
+// kernels scale each group's dot product in fp32 and subtract the
+// (bias + z) * sum(x) term separately, so one v_and_or_b32 per pair is all the
+// per-element work.
+template <typename DT>
+struct Raw;
+template <>
+struct Raw<F16> {
+  static constexpr uint32_t kMagic = 0x64006400u;  // (1024, 1024)
+  static constexpr uint32_t kOnes = 0x3C003C00u;   // (1, 1)
+  static constexpr float kBias = 1024.f;
+};
+template <>
+struct Raw<BF16> {
+  static constexpr uint32_t kMagic = 0x43004300u;  // (128, 128)
+  static constexpr uint32_t kOnes = 0x3F803F80u;   // (1, 1)
+  static constexpr float kBias = 128.f;
+};
+
+template <typename DT>
+__device__ __forceinline__ typename DT::vec8 biased_word(uint32_t w, uint32_t mask, uint32_t magic) {
+  const u32x4 r = {and_or(w, mask, magic), and_or(w >> 4, mask, magic), and_or(w >> 8, mask, magic),
+                   and_or(w >> 12, mask, magic)};
+  return __builtin_bit_cast(typename DT::vec8, r);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ uint32_t zero_nibble(uint64_t zw, int c) {
   return (uint32_t)(zw >> (4 * c)) & 0xFu;

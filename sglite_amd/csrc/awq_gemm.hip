@@ -2,16 +2,8 @@
 //
 // Two kernels share the CDNA4 tile layout (awq_device.h):
 //
-//  * skinny_kernel (decode, M <= 32): HBM-bound.  Each wave streams 1 KiB
-//    weight tiles (one 16-byte load per lane = four MFMA operands), dequantises
-//    in registers and feeds v_mfma_f32_16x16x32 with the weights as the A
-//    operand (16 columns) and up to 32 activation rows as the B operand.  A
-//    workgroup is 4 waves: WN along N times WK along K, with the WK partial
-//    sums reduced through LDS.  K is split over KS workgroups; their fp32
-//    partials go to a workspace and the last workgroup to finish (atomic
-//    arrival counter, reset by that workgroup) reduces them in a fixed order,
-//    adds the bias and stores, so one launch does the whole linear and the
-//    result is deterministic.
+//  * skinny_kernel (decode, M <= 32, awq_skinny.hip): HBM-bound split-K
+//    kernel, one launch per linear.
 //
 //  * tiled_kernel (prefill, M > 32): MFMA-bound.  A workgroup computes
 //    BM x 256 outputs; the activation tile (BM x 128 per k-step) is staged
@@ -26,172 +18,15 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "awq_device.h"
+#include "awq_epilogue.h"
 #include "awq_launch.h"
 
 namespace sgl_awq {
 
 namespace {
-
-template <typename DT>
-__device__ __forceinline__ void store4(typename DT::elem* __restrict__ out, const typename DT::elem* __restrict__ bias,
-                                       int64_t m, int64_t N, int64_t n0, f32x4 v) {
-  typename DT::vec4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = finish<DT>(v[i], bias, (int)(n0 + i));
-  *(typename DT::vec4*)(out + m * N + n0) = r;
-}
-
-// ---------------------------------------------------------------------------
-// Skinny split-K kernel.
-// ---------------------------------------------------------------------------
-template <int MT, int NTW, int WK, typename DT>
-__global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __restrict__ x,
-                                                     const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
-                                                     const uint64_t* __restrict__ z_r,
-                                                     const typename DT::elem* __restrict__ bias,
-                                                     typename DT::elem* __restrict__ out, float* __restrict__ part,
-                                                     int32_t* __restrict__ counters, int M, int N, int K, int NT,
-                                                     int KT, int NG, int gshift, int ktc, int KS) {
-  using E = typename DT::elem;
-  using V8 = typename DT::vec8;
-  using ZS = typename Dq<DT>::ZS;
-  constexpr int WN = 4 / WK;
-  constexpr int NTG = WN * NTW;
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int wn = wave % WN, wk = wave / WN;
-  const int c = lane & 15, lg = lane >> 4;
-  const int nt0 = blockIdx.x * NTG + wn * NTW;
-  const int kt_begin = blockIdx.y * ktc;
-  const int kt_end = min(kt_begin + ktc, KT);
-
-  f32x4 acc[MT][NTW];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const E* xrow[MT];
-  bool mval[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + c;
-    mval[mt] = m < M;
-    xrow[mt] = x + (int64_t)min(m, M - 1) * K + lg * 8;
-  }
-  const u32x4* wbase[NTW];
-  int ntc[NTW];
-#pragma unroll
-  for (int j = 0; j < NTW; ++j) {
-    ntc[j] = min(nt0 + j, NT - 1);  // columns past N read a valid tile and are never stored
-    wbase[j] = wt + (int64_t)ntc[j] * KT * 64 + lane;
-  }
-
-  for (int kt = kt_begin + wk; kt < kt_end; kt += WK) {
-    u32x4 q[NTW];
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) q[j] = __builtin_nontemporal_load(wbase[j] + (int64_t)kt * 64);
-    int gprev = -1;
-    ZS zs[NTW];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int kb = kt * 128 + 32 * w;
-      if (kb >= K) break;
-      const int g = kb >> gshift;
-      if (g != gprev) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          const int64_t gi = (int64_t)ntc[j] * NG + g;
-          zs[j] = Dq<DT>::make(zero_nibble(z_r[gi], c), s_r[gi * 16 + c]);
-        }
-        gprev = g;
-      }
-      V8 xb[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const V8 v = *(const V8*)(xrow[mt] + kb);
-        xb[mt] = mval[mt] ? v : V8{};
-      }
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const V8 a = Dq<DT>::word(q[j][w], zs[j]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][j] = mfma16x16x32(a, xb[mt], acc[mt][j]);
-      }
-    }
-  }
-
-  // Reduce the WK waves that share columns.
-  if constexpr (WK > 1) {
-    __shared__ f32x4 red[(WK - 1) * WN * MT * NTW * 64];
-    if (wk > 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) red[((((wk - 1) * WN + wn) * MT + mt) * NTW + j) * 64 + lane] = acc[mt][j];
-    }
-    __syncthreads();
-    if (wk == 0) {
-#pragma unroll
-      for (int o = 0; o < WK - 1; ++o)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int j = 0; j < NTW; ++j) acc[mt][j] += red[(((o * WN + wn) * MT + mt) * NTW + j) * 64 + lane];
-    }
-  }
-
-  // Output fragment of (mt, j): row m = 16*mt + c, columns n0..n0+3.
-  if (KS == 1) {
-    if (wk == 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          const int m = mt * 16 + c;
-          const int n0 = (nt0 + j) * 16 + 4 * lg;
-          if (m < M && n0 < N) store4<DT>(out, bias, m, N, n0, acc[mt][j]);
-        }
-    }
-    return;
-  }
-
-  const int64_t Np = (int64_t)NT * 16;
-  if (wk == 0) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const int m = mt * 16 + c;
-        const int n0 = (nt0 + j) * 16 + 4 * lg;
-        if (m < M && n0 < Np) *(f32x4*)(part + ((int64_t)blockIdx.y * M + m) * Np + n0) = acc[mt][j];
-      }
-  }
-  __threadfence();  // publish this thread's partials device-wide (all XCDs)
-  __syncthreads();
-  __shared__ int s_last;
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(&counters[blockIdx.x], 1);
-    s_last = (prev == KS - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();  // acquire the other workgroups' partials
-
-  constexpr int QPR = NTG * 4;  // float4 quads per row of this column group
-  const int64_t nbase = (int64_t)blockIdx.x * NTG * 16;
-  for (int idx = threadIdx.x; idx < M * QPR; idx += 256) {
-    const int m = idx / QPR;
-    const int64_t n0 = nbase + 4 * (idx % QPR);
-    if (n0 >= N) continue;
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int ks = 0; ks < KS; ++ks) s += *(const f32x4*)(part + ((int64_t)ks * M + m) * Np + n0);
-    store4<DT>(out, bias, m, N, n0, s);
-  }
-  if (threadIdx.x == 0) counters[blockIdx.x] = 0;  // ready for the next call
-}
 
 // ---------------------------------------------------------------------------
 // Tiled MFMA kernel: BM x 256 per workgroup, 4 waves of BM x 64.
@@ -325,37 +160,6 @@ int env_int(const char* name, int dflt) {
 }
 
 template <typename DT>
-hipError_t launch_skinny_dt(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                            const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, hipStream_t s) {
-  using E = typename DT::elem;
-  const uint16_t* sbase = (const uint16_t*)sr;
-  const uint64_t* zbase = (const uint64_t*)zr;
-  const int mt = (g.M + 15) / 16;
-  const int ntw = p.variant / 10, wk = p.variant % 10;
-  dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
-#define SGL_SKINNY(MT_, NTW_, WK_)                                                                               \
-  if (mt == MT_ && ntw == NTW_ && wk == WK_) {                                                                 \
-    hipLaunchKernelGGL((skinny_kernel<MT_, NTW_, WK_, DT>), grid, dim3(256), 0, s, (const E*)x, (const u32x4*)w, \
-                       sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters, (int)g.M, (int)g.N, (int)g.K, \
-                       (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);                                \
-    return hipGetLastError();                                                                                  \
-  }
-#define SGL_SKINNY_MT(NTW_, WK_) SGL_SKINNY(1, NTW_, WK_) SGL_SKINNY(2, NTW_, WK_)
-  SGL_SKINNY_MT(1, 1)
-  SGL_SKINNY_MT(1, 2)
-  SGL_SKINNY_MT(1, 4)
-  SGL_SKINNY_MT(2, 1)
-  SGL_SKINNY_MT(2, 2)
-  SGL_SKINNY_MT(2, 4)
-  SGL_SKINNY_MT(4, 1)
-  SGL_SKINNY_MT(4, 2)
-  SGL_SKINNY_MT(4, 4)
-#undef SGL_SKINNY_MT
-#undef SGL_SKINNY
-  return hipErrorInvalidValue;
-}
-
-template <typename DT>
 hipError_t launch_tiled_dt(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                            const void* bias, void* out, const Geom& g, hipStream_t s) {
   using E = typename DT::elem;
@@ -388,7 +192,7 @@ GemmPlan plan_gemm(const Geom& g) {
     const int64_t ng1 = (g.NT + 3) / 4;
     if (ng1 < kNumCU) wk = 4;
     const int env = env_int("SGL_AWQ_SKINNY_VARIANT", 0);
-    if (env > 0) {
+    if (env == 11 || env == 12 || env == 14 || env == 21 || env == 22 || env == 41) {
       ntw = env / 10;
       wk = env % 10;
     }
@@ -428,10 +232,7 @@ GemmPlan plan_gemm(const Geom& g) {
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s) {
-  if (p.kind == 0) {
-    return dtype == 0 ? launch_skinny_dt<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, s)
-                      : launch_skinny_dt<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, s);
-  }
+  if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
   return dtype == 0 ? launch_tiled_dt<F16>(p, x, w, sr, zr, bias, out, g, s)
                     : launch_tiled_dt<BF16>(p, x, w, sr, zr, bias, out, g, s);
 }

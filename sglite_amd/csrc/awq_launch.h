@@ -34,6 +34,9 @@ struct GemmPlan {
 };
 
 GemmPlan plan_gemm(const Geom& g);
+hipError_t launch_skinny(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                         hipStream_t s);
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);

@@ -1,0 +1,337 @@
+// Decode-regime W4A16 kernel (M <= 32) for gfx950.  HBM-bound: one launch
+// streams the int4 weights once, dequantises in registers and reduces split-K
+// partials across workgroups without cache-wide fences.  Built with
+// -mllvm -amdgpu-mfma-vgpr-form so MFMA results stay in VGPRs, where the fp32
+// group scaling reads them.
+//
+// Replaces awq_gemm_kernel / awq_gemm_triton
+// (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
+// and gptq_marlin_gemm (marlin_utils.py:388-410) for small batches.
+#include <type_traits>
+
+#include "awq_device.h"
+#include "awq_epilogue.h"
+#include "awq_launch.h"
+
+namespace sgl_awq {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Skinny split-K kernel.
+//
+// Each wave owns NTW column tiles and the k-tiles kt_begin + wk + WK*i of its
+// workgroup's k-range, processed in batches of D tiles whose loads (weights,
+// scales, zero words, activation fragments) are all issued before any is
+// consumed.  GPT is the number of quantisation groups one 128-row tile spans
+// (1 for G >= 128, 2 for G = 64, 4 for G = 32).
+//
+// Arithmetic per group g (rows k of the group, column n, batch row m):
+//   sum_k (q - z) s x = s * (C[n][m] - (B + z) * S[m]),
+//   C = sum_k (B + q) x   (v_mfma_f32_16x16x32 on the biased operand, B = 1024
+//                          for fp16, 128 for bf16, built by one v_and_or per pair)
+//   S = sum_k x           (the same MFMA with an all-ones operand)
+// s * C is added to the fp32 accumulator right away (v_fma_mix, scale rows of
+// the output fragment); the -s (B + z) * S terms of four groups at a time are
+// one v_mfma_f32_16x16x4_f32 whose A operand holds -s (B + z) (exact in fp32)
+// for the lane's own column and group slot, and whose B operand holds S of
+// that slot.  So per weight pair the kernel executes a single VALU op.
+//
+// Split-K handoff between workgroups (possibly on different XCDs, whose L2s
+// are not coherent with each other) uses device-scope atomics only: partials
+// are written with returning atomic exchanges (complete at the device
+// coherence point before the value returns), the arrival counter is a
+// device-scope fetch-add, and the last workgroup reads the partials back with
+// atomic exchanges.  No agent-scope fence -- i.e. no L2 writeback/invalidate
+// -- is executed.  The reduction order is fixed (ks = 0, 1, ...), so results
+// are deterministic.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xchg_agent(float* p, float v) {
+  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MT, int NTW, int WK, int GPT, typename DT>
+__global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __restrict__ x,
+                                                     const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
+                                                     const uint64_t* __restrict__ z_r,
+                                                     const typename DT::elem* __restrict__ bias,
+                                                     typename DT::elem* __restrict__ out, float* __restrict__ part,
+                                                     int32_t* __restrict__ counters, int M, int N, int K, int NT,
+                                                     int KT, int NG, int gshift, int ktc, int KS) {
+  using E = typename DT::elem;
+  using V8 = typename DT::vec8;
+  using V4 = typename DT::vec4;
+  constexpr int WN = 4 / WK;
+  constexpr int NTG = WN * NTW;
+  constexpr int D = NTW >= 4 ? 1 : 4 / NTW;  // k-tiles per batch
+  constexpr int BPG = 4 / GPT;               // 32-row k-blocks per group
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wn = wave % WN, wk = wave / WN;
+  const int c = lane & 15, lg = lane >> 4;
+  const int nt0 = blockIdx.x * NTG + wn * NTW;
+  const int kt_begin = blockIdx.y * ktc;
+  const int kt_end = min(kt_begin + ktc, KT);
+  const int first = kt_begin + wk;
+  const int niter = first < kt_end ? (kt_end - first + WK - 1) / WK : 0;
+  // Tiles below kt_full have all 128 rows inside K; only the last tile of a
+  // K that is not a multiple of 128 needs its tail k-blocks masked.
+  const int kt_full = K >> 7;
+  int nfull = niter;
+  if (niter > 0 && first + WK * (niter - 1) >= kt_full) --nfull;
+
+  f32x4 acc[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t kMask = opaque_vgpr(0x000F000Fu), kMagic = opaque_vgpr(Raw<DT>::kMagic);
+  const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Slot-selecting ones: operand row n (= lane column c) is all ones iff
+  // n / 4 == slot, so sum(x) of the group in slot i lands in output rows
+  // 4i..4i+3, i.e. in the lanes with lg == i -- the lanes that hold slot i of
+  // the correction MFMA's B operand.  No per-lane select is needed.
+  V8 sel[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = (c >> 2) == i ? Raw<DT>::kOnes : 0u;
+    sel[i] = __builtin_bit_cast(V8, u32x4{o, o, o, o});
+  }
+
+  // 32-bit byte offsets from uniform bases (rows past M re-read row M-1;
+  // their outputs are never stored).  The host keeps every buffer below 4 GiB.
+  uint32_t xoff[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xoff[mt] = ((uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)K + lg * 8) * 2u;
+  uint32_t woff[NTW], srow_off[NTW], sown_off[NTW], zoff[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const uint32_t ntc = (uint32_t)min(nt0 + j, NT - 1);  // columns past N read a valid tile, never stored
+    woff[j] = (ntc * (uint32_t)KT * 64u + lane) * 16u;
+    srow_off[j] = (ntc * (uint32_t)NG * 16u + 4u * lg) * 2u;  // scales of output rows 4lg..4lg+3
+    sown_off[j] = (ntc * (uint32_t)NG * 16u + c) * 2u;        // scale of the lane's own column
+    zoff[j] = ntc * (uint32_t)NG * 8u;
+  }
+  auto group_of = [&](int kt, int gg) -> uint32_t {
+    return (uint32_t)min((kt * 128 + 32 * gg * BPG) >> gshift, NG - 1);
+  };
+
+  // A batch covers NB tiles = NB * GPT groups; group p of the batch sits in
+  // correction slot p % 4 of flush block p / 4.
+  auto run_batch = [&](auto NBc, int i_first, bool masked) {
+    constexpr int NB = decltype(NBc)::value;
+    constexpr int NGR = NB * GPT;          // groups in the batch
+    constexpr int NFB = (NGR + 3) / 4;     // correction flushes
+    u32x4 q[NB][NTW];
+    V4 srow[NB][NTW][GPT];
+    V8 xb[NB][4][MT];
+    float corrA[NFB][NTW];
+#pragma unroll
+    for (int d = 0; d < NB; ++d) {
+      const int kt = first + WK * (i_first + d);
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) q[d][j] = ld_off_nt<u32x4>(wt, woff[j] + (uint32_t)kt * 1024u);
+#pragma unroll
+      for (int gg = 0; gg < GPT; ++gg) {
+        const uint32_t g = group_of(kt, gg);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) srow[d][j][gg] = ld_off<V4>(s_r, srow_off[j] + g * 32u);
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const int kb = kt * 128 + 32 * w;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if (masked) {
+            const bool kv = kb < K;  // k-blocks past K read zeros
+            const V8 v = ld_off<V8>(x, xoff[mt] + (uint32_t)(kv ? kb : 0) * 2u);
+            xb[d][w][mt] = kv ? v : V8{};
+          } else {
+            xb[d][w][mt] = ld_off<V8>(x, xoff[mt] + (uint32_t)kb * 2u);
+          }
+        }
+      }
+    }
+    // Correction A operand: lane (c, lg) takes -s (B + z) of its own column for
+    // the group in slot lg of each flush block (slots past the batch read a
+    // valid group; their sum(x) rows are zero).
+#pragma unroll
+    for (int f = 0; f < NFB; ++f) {
+      const int p = min(f * 4 + lg, NGR - 1);
+      const int kt = first + WK * (i_first + p / GPT);
+      const uint32_t g = group_of(kt, p % GPT);
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const E sv = ld_off<E>(s_r, sown_off[j] + g * 32u);
+        const uint64_t zw = ld_off<uint64_t>(z_r, zoff[j] + g * 8u);
+        corrA[f][j] = -(float)sv * (Raw<DT>::kBias + (float)zero_nibble(zw, c));
+      }
+    }
+    // Keep the whole batch's loads ahead of its compute (the scheduler would
+    // otherwise interleave them to save registers, serialising the latency).
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 cs[MT];
+#pragma unroll
+    for (int d = 0; d < NB; ++d)
+#pragma unroll
+      for (int gg = 0; gg < GPT; ++gg) {
+        const int p = d * GPT + gg, slot = p & 3;
+        f32x4 cm[MT][NTW];
+#pragma unroll
+        for (int b = 0; b < BPG; ++b) {
+          const int w = gg * BPG + b;
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) {
+            const V8 a = biased_word<DT>(q[d][j][w], kMask, kMagic);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) cm[mt][j] = mfma16x16x32(a, xb[d][w][mt], b == 0 ? zero4 : cm[mt][j]);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            cs[mt] = mfma16x16x32(sel[slot], xb[d][w][mt], (slot == 0 && b == 0) ? zero4 : cs[mt]);
+        }
+        // s * C onto the accumulator (output rows 4lg + r).
+#pragma unroll
+        for (int j = 0; j < NTW; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float sr = (float)srow[d][j][gg][r];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][j][r] = __builtin_fmaf(sr, cm[mt][j][r], acc[mt][j][r]);
+          }
+        if (slot == 3 || p == NGR - 1) {  // fold the block's -s (B + z) * sum(x) terms
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x4f32(corrA[p >> 2][j], cs[mt][0], acc[mt][j]);
+        }
+      }
+  };
+
+  // Main loop: batches of D fully-valid tiles; remainder one tile at a time.
+  int i0 = 0;
+  for (; i0 + D <= nfull; i0 += D) run_batch(std::integral_constant<int, D>{}, i0, false);
+  for (int i = i0; i < niter; ++i) run_batch(std::integral_constant<int, 1>{}, i, i >= nfull);
+
+  // Reduce the WK waves that share columns.
+  if constexpr (WK > 1) {
+    __shared__ f32x4 red[(WK - 1) * WN * MT * NTW * 64];
+    if (wk > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) red[((((wk - 1) * WN + wn) * MT + mt) * NTW + j) * 64 + lane] = acc[mt][j];
+    }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int o = 0; o < WK - 1; ++o)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) acc[mt][j] += red[(((o * WN + wn) * MT + mt) * NTW + j) * 64 + lane];
+    }
+  }
+
+  // Output fragment of (mt, j): row m = 16*mt + c, columns n0..n0+3.
+  if (KS == 1) {
+    if (wk == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const int m = mt * 16 + c;
+          const int n0 = (nt0 + j) * 16 + 4 * lg;
+          if (m < M && n0 < N) store4<DT>(out, bias, m, N, n0, acc[mt][j]);
+        }
+    }
+    return;
+  }
+
+  const int64_t Np = (int64_t)NT * 16;
+  if (wk == 0) {
+    float chk = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const int m = mt * 16 + c;
+        const int n0 = (nt0 + j) * 16 + 4 * lg;
+        if (m < M && n0 < Np) {
+          float* p = part + ((int64_t)blockIdx.y * M + m) * Np + n0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) chk += xchg_agent(p + r, acc[mt][j][r]);
+        }
+      }
+    // Consuming the returned values makes the wave wait until every
+    // exchange has been performed before it reaches the barrier.
+    asm volatile("" ::"v"(chk));
+  }
+  __syncthreads();
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == KS - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  constexpr int QPR = NTG * 4;  // float4 quads per row of this column group
+  const int64_t nbase = (int64_t)blockIdx.x * NTG * 16;
+  for (int idx = threadIdx.x; idx < M * QPR; idx += 256) {
+    const int m = idx / QPR;
+    const int64_t n0 = nbase + 4 * (idx % QPR);
+    if (n0 >= N) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) {
+      float* p = part + ((int64_t)ks * M + m) * Np + n0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sum[r] += xchg_agent(p + r, 0.f);
+    }
+    store4<DT>(out, bias, m, N, n0, sum);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename DT>
+hipError_t launch_skinny_dt_impl(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                            const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, hipStream_t s) {
+  using E = typename DT::elem;
+  const uint16_t* sbase = (const uint16_t*)sr;
+  const uint64_t* zbase = (const uint64_t*)zr;
+  const int mt = (g.M + 15) / 16;
+  const int ntw = p.variant / 10, wk = p.variant % 10;
+  const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
+  dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
+#define SGL_SKINNY(MT_, NTW_, WK_, GPT_)                                                                         \
+  if (mt == MT_ && ntw == NTW_ && wk == WK_ && gpt == GPT_) {                                                  \
+    hipLaunchKernelGGL((skinny_kernel<MT_, NTW_, WK_, GPT_, DT>), grid, dim3(256), 0, s, (const E*)x,          \
+                       (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters, (int)g.M,   \
+                       (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);            \
+    return hipGetLastError();                                                                                  \
+  }
+#define SGL_SKINNY_G(MT_, NTW_, WK_) SGL_SKINNY(MT_, NTW_, WK_, 1) SGL_SKINNY(MT_, NTW_, WK_, 2) SGL_SKINNY(MT_, NTW_, WK_, 4)
+#define SGL_SKINNY_MT(NTW_, WK_) SGL_SKINNY_G(1, NTW_, WK_) SGL_SKINNY_G(2, NTW_, WK_)
+  SGL_SKINNY_MT(1, 1)
+  SGL_SKINNY_MT(1, 2)
+  SGL_SKINNY_MT(1, 4)
+  SGL_SKINNY_MT(2, 1)
+  SGL_SKINNY_MT(2, 2)
+  SGL_SKINNY_MT(4, 1)
+#undef SGL_SKINNY_MT
+#undef SGL_SKINNY_G
+#undef SGL_SKINNY
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_skinny(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                         hipStream_t s) {
+  return dtype == 0 ? launch_skinny_dt_impl<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, s)
+                    : launch_skinny_dt_impl<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, s);
+}
+
+}  // namespace sgl_awq

@@ -168,7 +168,7 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
         _require_cuda(bias)
         if bias.numel() != N:
             raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
-        bias = bias.to(x.dtype).contiguous()
+        bias = _aligned(bias.to(x.dtype).reshape(-1), 8)
     if out is None:
         out = torch.empty((M, N), dtype=x.dtype, device=dev)
     lib = _lib.load()
