@@ -186,11 +186,17 @@ GemmPlan plan_gemm(const Geom& g) {
   GemmPlan p{};
   if (g.M <= 32) {
     p.kind = 0;
-    // Defaults: 4 waves along N (one 16-column tile each, sharing activation
-    // fragments through L1) for wide layers; waves along K for narrow ones.
-    int ntw = 1, wk = 1;
-    const int64_t ng1 = (g.NT + 3) / 4;
-    if (ng1 < kNumCU) wk = 4;
+    // Measured on MI355X over the Qwen3-4B / Llama-3-8B decode shapes:
+    // wide layers (>= 1024 column tiles) run best with two tiles per wave and
+    // 2 x 2 waves per workgroup; narrower ones with one column tile per
+    // workgroup and K split over its 4 waves.  Cross-workgroup split-K costs
+    // a few device-scope atomic round trips (~1-3 us), so it is only used
+    // when there are too few column tiles to occupy the GPU.
+    int ntw = 1, wk = 4;
+    if (g.NT >= 1024) {
+      ntw = 2;
+      wk = g.M <= 8 ? 2 : 1;
+    }
     const int env = env_int("SGL_AWQ_SKINNY_VARIANT", 0);
     if (env == 11 || env == 12 || env == 14 || env == 21 || env == 22 || env == 41) {
       ntw = env / 10;
@@ -200,13 +206,15 @@ GemmPlan plan_gemm(const Geom& g) {
     const int64_t ntg = (int64_t)wn * ntw;
     p.variant = ntw * 10 + wk;
     p.grid_x = (g.NT + ntg - 1) / ntg;
-    // Split K so that about 2 workgroups per CU are in flight, keeping at
-    // least 2 k-tiles per wave and the partial traffic well below the
-    // weight traffic (KS * M * N * 8 bytes vs K * N / 2).
-    int64_t ks = (2 * kNumCU + p.grid_x - 1) / p.grid_x;
-    const int64_t ks_traffic = std::max<int64_t>(1, g.K / (64 * g.M));
-    const int64_t ks_len = std::max<int64_t>(1, g.KT / (2 * wk));
-    ks = std::min(ks, std::min(ks_traffic, ks_len));
+    int64_t ks = 1;
+    if (p.grid_x < kNumCU / 2) {
+      // Few column tiles: split K so about one workgroup per CU is busy,
+      // keeping >= 4 k-tiles per wave and the partial traffic
+      // (KS * M * N * 8 bytes) below a quarter of the weight stream.
+      ks = (kNumCU + p.grid_x - 1) / p.grid_x;
+      ks = std::min(ks, std::max<int64_t>(1, g.KT / (4 * wk)));
+      ks = std::min(ks, std::max<int64_t>(1, g.K / (64 * g.M)));
+    }
     const int env_ks = env_int("SGL_AWQ_SKINNY_KS", 0);
     if (env_ks > 0) ks = env_ks;
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));

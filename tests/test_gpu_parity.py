@@ -153,7 +153,7 @@ def test_gemm_golden_fixtures():
 
 def test_split_k_is_deterministic():
     ops = _ops()
-    K, N, G = 4096, 2560, 128  # narrow layer: the plan splits K across workgroups
+    K, N, G = 8192, 512, 128  # few column tiles: the plan splits K across workgroups
     _, d = _linear(K, N, G, seed=500)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
@@ -258,10 +258,11 @@ def test_apply_without_processing_repacks_on_the_fly():
     assert ok, (err, mx)
 
 
+@pytest.mark.parametrize("K,N", [(4096, 2560), (8192, 512)])
 @pytest.mark.parametrize("M", [1, 8, 64])
-def test_hip_graph_capture_replays(M):
+def test_hip_graph_capture_replays(M, K, N):
     ops = _ops()
-    K, N, G = 4096, 2560, 128
+    G = 128
     _, d = _linear(K, N, G, seed=1000 + M)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
@@ -285,3 +286,41 @@ def test_hip_graph_capture_replays(M):
         torch.cuda.synchronize()
         assert torch.equal(z, eager)
     assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("variant", [11, 12, 14, 21, 22, 41])
+@pytest.mark.parametrize("G", [128, 64, 32])
+def test_every_decode_variant(variant, G, monkeypatch):
+    """Each decode-kernel instantiation, with and without cross-workgroup
+    split-K, on a K that gives every wave full batches plus a masked tail."""
+    ops = _ops()
+    K, N = 2336, 200  # K % 128 == 32: the last k-tile is partial; N % 16 == 8
+    t, d = _linear(K, N, G, seed=variant * 7 + G)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    for ks in (1, 3):
+        monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
+        monkeypatch.setenv("SGL_AWQ_SKINNY_KS", str(ks))
+        for M in (1, 9, 17, 32):
+            x = oracle.make_activation(M, K, seed=M + ks)
+            y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
+            ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+            ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+            assert ok, (variant, G, ks, M, err, mx)
+        assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("M", [1, 20])
+def test_decode_bf16_variants(M, monkeypatch):
+    ops = _ops()
+    K, N, G = 2304, 136, 64
+    t, d = _linear(K, N, G, seed=77 + M, dtype=torch.bfloat16)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    x = oracle.make_activation(M, K, seed=78, dtype=torch.bfloat16)
+    ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+    for variant in (14, 22, 41):
+        monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
+        y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
+        ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+        assert ok, (variant, err, mx)

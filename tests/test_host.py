@@ -102,7 +102,7 @@ def test_null_and_misaligned_pointers_rejected():
 def test_missing_workspace_is_reported_before_launch():
     lib = _lib.load()
     fake = 0x10000
-    K, N, M = 4096, 2560, 1
+    K, N, M = 8192, 512, 1  # 32 column tiles: the plan splits K across workgroups
     need = lib.awq_workspace_bytes(M, N, K, 128)
     assert need > 0
     st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, None, 0, None, None)
