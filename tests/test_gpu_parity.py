@@ -294,7 +294,9 @@ def test_every_decode_variant(variant, G, monkeypatch):
     """Each decode-kernel instantiation, with and without cross-workgroup
     split-K, on a K that gives every wave full batches plus a masked tail."""
     ops = _ops()
-    K, N = 2336, 200  # K % 128 == 32: the last k-tile is partial; N % 16 == 8
+    # K % G == 0 with a partial last 128-row tile where G allows; N % 16 == 8
+    K = {32: 2336, 64: 2368, 128: 2432}[G]
+    N = 200
     t, d = _linear(K, N, G, seed=variant * 7 + G)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
