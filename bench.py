@@ -98,22 +98,25 @@ def time_replays(graphs, n: int) -> float:
     return a.elapsed_time(b)
 
 
-def cpu_baseline() -> dict:
+def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 30) -> dict:
+    """The CPU oracle on the same layer, repeated until about ``min_seconds`` of work."""
     from oracle import awq_oracle as oracle
 
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
-    total_b, total_t = 0, 0.0
+    total_b, total_t, passes = 0, 0.0, 0
     warm = oracle.make_awq_linear(256, 256, G, seed=0)
     oracle.awq_gemm(oracle.make_activation(1, 256, 0), warm["qweight"], warm["qzeros"], warm["scales"], None, G)
-    for i, (_, K, N) in enumerate(LAYER):
-        t = oracle.make_awq_linear(K, N, G, seed=i)
-        for M in M_SET:
-            x = oracle.make_activation(M, K, seed=100 + M)
-            t0 = time.perf_counter()
-            oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
-            total_t += time.perf_counter() - t0
-            total_b += gemm_bytes(M, N, K)
+    tensors = [oracle.make_awq_linear(K, N, G, seed=i) for i, (_, K, N) in enumerate(LAYER)]
+    xs = {(M, K): oracle.make_activation(M, K, seed=100 + M) for M in M_SET for _, K, _ in LAYER}
+    while passes < max_passes and (passes == 0 or total_t < min_seconds):
+        for t, (_, K, N) in zip(tensors, LAYER):
+            for M in M_SET:
+                t0 = time.perf_counter()
+                oracle.awq_gemm(xs[(M, K)], t["qweight"], t["qzeros"], t["scales"], None, G)
+                total_t += time.perf_counter() - t0
+                total_b += gemm_bytes(M, N, K)
+        passes += 1
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -125,7 +128,52 @@ def cpu_baseline() -> dict:
         pass
     return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": "CPU oracle (numpy unpack + dequantise, fp32 torch matmul, fp16 cast) over the same layer's "
-                      f"4 linears at M=1,8,32, one pass each ({total_t:.1f} s); host {model}"}
+                      f"4 linears at M=1,8,32, {passes} passes ({total_t:.1f} s); host {model}"}
+
+
+def rocprof_summary(trace_dir: str, command: str) -> str:
+    """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
+
+    The decode phase launches every (M, linear) of the layer equally often,
+    so the mean algorithmic bytes per decode launch is step_bytes / 12 and
+    the roofline figure is that over the mean skinny_kernel duration.
+    """
+    import csv
+    import glob
+    from collections import defaultdict
+
+    path = sorted(glob.glob(os.path.join(trace_dir, "*kernel_trace.csv")))[0]
+    rows = list(csv.DictReader(open(path)))
+    groups = defaultdict(list)
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "skinny_kernel" not in name and "tiled_kernel" not in name:
+            continue
+        short = name.replace("(anonymous namespace)::", "").replace("sgl_awq::", "").replace("void ", "")
+        short = short[:short.index("(")] if "(" in short else short
+        key = (short, r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"])
+        groups[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    n_lin = len(M_SET) * len(LAYER)
+    step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
+    sk = [d for (k, *_), ds in groups.items() if k.startswith("skinny") for d in ds]
+    mean_us = sum(sk) / len(sk)
+    mean_b = step_bytes / n_lin
+    lines = [
+        "# Decode kernel (skinny_kernel) on the Qwen3-4B layer workload, rocprofv3 kernel trace",
+        "",
+        f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
+        "",
+        f"skinny_kernel dispatches: {len(sk)}, mean duration {mean_us:.3f} us; mean algorithmic bytes per "
+        f"launch {mean_b / 1e6:.3f} MB (step bytes {step_bytes} / {n_lin} launches); "
+        f"achieved {mean_b / mean_us / 1e3:.1f} GB/s = {mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.",
+        "",
+        "| kernel | grid (x, y) | block | dispatches | mean us | min us | max us |",
+        "|---|---|---|---|---|---|---|",
+    ]
+    for (name, gx, gy, bx), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {int(gx) // int(bx)}, {gy} | {bx} | {len(ds)} | {sum(ds) / len(ds):.2f} | "
+                     f"{min(ds):.2f} | {max(ds):.2f} |")
+    return "\n".join(lines) + "\n"
 
 
 def main() -> int:
@@ -136,7 +184,14 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=36, help="distinct weight copies rotated through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--rocprof-summary", metavar="TRACE_DIR",
+                    help="print a markdown summary of a rocprofv3 --kernel-trace run of this script and exit")
+    ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
+                                                  "python3 bench.py --steps 500 --no-cpu-baseline")
     args = ap.parse_args()
+    if args.rocprof_summary:
+        print(rocprof_summary(args.rocprof_summary, args.rocprof_command), end="")
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
               "design, not a measured path", file=sys.stderr)
