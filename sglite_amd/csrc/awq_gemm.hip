@@ -159,6 +159,17 @@ int env_int(const char* name, int dflt) {
   return (v && *v) ? atoi(v) : dflt;
 }
 
+// Decode-kernel shapes that are instantiated (ntw * 10000 + wn * 100 + wk).
+bool skinny_variant_ok(int v) {
+  switch (v) {
+    case 10104: case 10108: case 10116: case 10202: case 10401: case 10404:
+    case 20202: case 20401: case 20204:
+      return true;
+    default:
+      return false;
+  }
+}
+
 template <typename DT>
 hipError_t launch_tiled_dt(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                            const void* bias, void* out, const Geom& g, hipStream_t s) {
@@ -186,25 +197,32 @@ GemmPlan plan_gemm(const Geom& g) {
   GemmPlan p{};
   if (g.M <= 32) {
     p.kind = 0;
-    // Measured on MI355X over the Qwen3-4B / Llama-3-8B decode shapes:
-    // wide layers (>= 1024 column tiles) run best with two tiles per wave and
-    // 2 x 2 waves per workgroup; narrower ones with one column tile per
-    // workgroup and K split over its 4 waves.  Cross-workgroup split-K costs
-    // a few device-scope atomic round trips (~1-3 us), so it is only used
-    // when there are too few column tiles to occupy the GPU.
-    int ntw = 1, wk = 4;
+    // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all
+    // variants over the Qwen3-4B and Llama-3-8B decode shapes on MI355X:
+    // wide layers (>= 1024 column tiles) use two column tiles per wave;
+    // narrower ones put one column tile per workgroup and split K over 4-16
+    // waves, more of them for short or very long K.
+    int ntw = 1, wn = 1, wk = 4;
     if (g.NT >= 1024) {
       ntw = 2;
+      wn = g.M <= 8 ? 2 : 4;
       wk = g.M <= 8 ? 2 : 1;
+    } else if (g.M > 16 && g.NT >= 384) {
+      wn = 2;
+      wk = 2;
+    } else if (g.KT <= 24 || g.KT >= 64) {
+      wk = 16;
+    } else {
+      wk = g.M <= 8 ? 4 : (g.M <= 16 ? 8 : 16);
     }
     const int env = env_int("SGL_AWQ_SKINNY_VARIANT", 0);
-    if (env == 11 || env == 12 || env == 14 || env == 21 || env == 22 || env == 41) {
-      ntw = env / 10;
-      wk = env % 10;
+    if (skinny_variant_ok(env)) {
+      ntw = env / 10000;
+      wn = (env / 100) % 100;
+      wk = env % 100;
     }
-    const int wn = 4 / wk;
     const int64_t ntg = (int64_t)wn * ntw;
-    p.variant = ntw * 10 + wk;
+    p.variant = ntw * 10000 + wn * 100 + wk;
     p.grid_x = (g.NT + ntg - 1) / ntg;
     int64_t ks = 1;
     if (p.grid_x < kNumCU / 2) {
@@ -212,7 +230,7 @@ GemmPlan plan_gemm(const Geom& g) {
       // keeping >= 4 k-tiles per wave and the partial traffic
       // (KS * M * N * 8 bytes) below a quarter of the weight stream.
       ks = (kNumCU + p.grid_x - 1) / p.grid_x;
-      ks = std::min(ks, std::max<int64_t>(1, g.KT / (4 * wk)));
+      ks = std::min(ks, std::max<int64_t>(1, g.KT / (2 * wk)));
       ks = std::min(ks, std::max<int64_t>(1, g.K / (64 * g.M)));
     }
     const int env_ks = env_int("SGL_AWQ_SKINNY_KS", 0);

@@ -50,21 +50,24 @@ __device__ __forceinline__ float xchg_agent(float* p, float v) {
   return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int MT, int NTW, int WK, int GPT, typename DT>
-__global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __restrict__ x,
-                                                     const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
-                                                     const uint64_t* __restrict__ z_r,
-                                                     const typename DT::elem* __restrict__ bias,
-                                                     typename DT::elem* __restrict__ out, float* __restrict__ part,
-                                                     int32_t* __restrict__ counters, int M, int N, int K, int NT,
-                                                     int KT, int NG, int gshift, int ktc, int KS) {
+template <int MT, int NTW, int WN, int WK, int GPT, typename DT>
+__global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
+    const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
+    const uint64_t* __restrict__ z_r, const typename DT::elem* __restrict__ bias, typename DT::elem* __restrict__ out,
+    float* __restrict__ part, int32_t* __restrict__ counters, int M, int N, int K, int NT, int KT, int NG, int gshift,
+    int ktc, int KS) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
   using V4 = typename DT::vec4;
-  constexpr int WN = 4 / WK;
+  constexpr int NTHREADS = 64 * WN * WK;
   constexpr int NTG = WN * NTW;
-  constexpr int D = NTW >= 4 ? 1 : 4 / NTW;  // k-tiles per batch
+  // k-tiles per batch: two batches of weights plus one of activation
+  // fragments must fit the register budget (128 VGPRs for >= 512 threads).
+  constexpr int D_BASE = NTHREADS >= 1024 ? 1 : NTHREADS >= 512 ? 2 : (NTW >= 4 ? 1 : 4 / NTW);
+  constexpr int D = D_BASE / MT > 0 ? D_BASE / MT : 1;
   constexpr int BPG = 4 / GPT;               // 32-row k-blocks per group
+  constexpr int NGR = D * GPT;               // groups per batch
+  constexpr int NFB = (NGR + 3) / 4;         // correction flushes per batch
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wn = wave % WN, wk = wave / WN;
@@ -74,11 +77,11 @@ __global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __
   const int kt_end = min(kt_begin + ktc, KT);
   const int first = kt_begin + wk;
   const int niter = first < kt_end ? (kt_end - first + WK - 1) / WK : 0;
-  // Tiles below kt_full have all 128 rows inside K; only the last tile of a
-  // K that is not a multiple of 128 needs its tail k-blocks masked.
-  const int kt_full = K >> 7;
-  int nfull = niter;
-  if (niter > 0 && first + WK * (niter - 1) >= kt_full) --nfull;
+  const int nbatch = (niter + D - 1) / D;
+  // Batches whose tiles all exist and lie fully inside K need no masking;
+  // only the last batch of a wave can hold missing tiles or the partial
+  // last k-tile of a K that is not a multiple of 128.
+  const bool last_masked = niter > 0 && (niter % D != 0 || first + WK * (niter - 1) >= (K >> 7));
 
   f32x4 acc[MT][NTW];
 #pragma unroll
@@ -92,9 +95,10 @@ __global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __
   // n / 4 == slot, so sum(x) of the group in slot i lands in output rows
   // 4i..4i+3, i.e. in the lanes with lg == i -- the lanes that hold slot i of
   // the correction MFMA's B operand.  No per-lane select is needed.
-  V8 sel[4];
+  constexpr int NSEL = NGR < 4 ? NGR : 4;  // slots a batch uses
+  V8 sel[NSEL];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NSEL; ++i) {
     const uint32_t o = (c >> 2) == i ? Raw<DT>::kOnes : 0u;
     sel[i] = __builtin_bit_cast(V8, u32x4{o, o, o, o});
   }
@@ -113,106 +117,136 @@ __global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __
     sown_off[j] = (ntc * (uint32_t)NG * 16u + c) * 2u;        // scale of the lane's own column
     zoff[j] = ntc * (uint32_t)NG * 8u;
   }
+  auto tile_kt = [&](int i) { return first + WK * min(i, niter - 1); };  // missing tiles reload the last one
   auto group_of = [&](int kt, int gg) -> uint32_t {
     return (uint32_t)min((kt * 128 + 32 * gg * BPG) >> gshift, NG - 1);
   };
 
-  // A batch covers NB tiles = NB * GPT groups; group p of the batch sits in
-  // correction slot p % 4 of flush block p / 4.
-  auto run_batch = [&](auto NBc, int i_first, bool masked) {
-    constexpr int NB = decltype(NBc)::value;
-    constexpr int NGR = NB * GPT;          // groups in the batch
-    constexpr int NFB = (NGR + 3) / 4;     // correction flushes
-    u32x4 q[NB][NTW];
-    V4 srow[NB][NTW][GPT];
-    V8 xb[NB][4][MT];
+  // Weight-side state of one batch (long-latency HBM loads, prefetched one
+  // batch ahead).  Group p of the batch sits in correction slot p % 4 of
+  // flush block p / 4.
+  struct WB {
+    V8 xb[D][4][MT];
+    u32x4 q[D][NTW];
+    V4 srow[D][NTW][GPT];
     float corrA[NFB][NTW];
+  };
+  auto load_w = [&](int bi, WB& w) {
 #pragma unroll
-    for (int d = 0; d < NB; ++d) {
-      const int kt = first + WK * (i_first + d);
+    for (int d = 0; d < D; ++d) {
+      const int kt = tile_kt(bi * D + d);
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) q[d][j] = ld_off_nt<u32x4>(wt, woff[j] + (uint32_t)kt * 1024u);
+      for (int j = 0; j < NTW; ++j) w.q[d][j] = ld_off_nt<u32x4>(wt, woff[j] + (uint32_t)kt * 1024u);
 #pragma unroll
       for (int gg = 0; gg < GPT; ++gg) {
         const uint32_t g = group_of(kt, gg);
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) srow[d][j][gg] = ld_off<V4>(s_r, srow_off[j] + g * 32u);
+        for (int j = 0; j < NTW; ++j) w.srow[d][j][gg] = ld_off<V4>(s_r, srow_off[j] + g * 32u);
       }
+    }
+    // Correction A operand: lane (c, lg) takes -s (B + z) of its own column
+    // for the group in slot lg of each flush block.
+#pragma unroll
+    for (int f = 0; f < NFB; ++f) {
+      const int pg = min(f * 4 + lg, NGR - 1);
+      const int kt = tile_kt(bi * D + pg / GPT);
+      const uint32_t g = group_of(kt, pg % GPT);
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const E sv = ld_off<E>(s_r, sown_off[j] + g * 32u);
+        const uint64_t zw = ld_off<uint64_t>(z_r, zoff[j] + g * 8u);
+        w.corrA[f][j] = -(float)sv * (Raw<DT>::kBias + (float)zero_nibble(zw, c));
+      }
+    }
+  };
+  // Activation fragments of one batch (L2-resident; loaded right before use,
+  // and issued before the next batch's weights so that waiting for them does
+  // not wait for those HBM loads -- loads return in issue order).
+  auto load_x = [&](int bi, V8 (&xb)[D][4][MT], bool masked) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int i = bi * D + d;
+      const int kt = tile_kt(i);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const int kb = kt * 128 + 32 * w;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          if (masked) {
-            const bool kv = kb < K;  // k-blocks past K read zeros
-            const V8 v = ld_off<V8>(x, xoff[mt] + (uint32_t)(kv ? kb : 0) * 2u);
-            xb[d][w][mt] = kv ? v : V8{};
+          if (masked) {  // missing tiles and k-blocks past K contribute zero
+            const bool ok = i < niter && kb < K;
+            const V8 v = ld_off<V8>(x, xoff[mt] + (uint32_t)(ok ? kb : 0) * 2u);
+            xb[d][w][mt] = ok ? v : V8{};
           } else {
             xb[d][w][mt] = ld_off<V8>(x, xoff[mt] + (uint32_t)kb * 2u);
           }
         }
       }
     }
-    // Correction A operand: lane (c, lg) takes -s (B + z) of its own column for
-    // the group in slot lg of each flush block (slots past the batch read a
-    // valid group; their sum(x) rows are zero).
-#pragma unroll
-    for (int f = 0; f < NFB; ++f) {
-      const int p = min(f * 4 + lg, NGR - 1);
-      const int kt = first + WK * (i_first + p / GPT);
-      const uint32_t g = group_of(kt, p % GPT);
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const E sv = ld_off<E>(s_r, sown_off[j] + g * 32u);
-        const uint64_t zw = ld_off<uint64_t>(z_r, zoff[j] + g * 8u);
-        corrA[f][j] = -(float)sv * (Raw<DT>::kBias + (float)zero_nibble(zw, c));
-      }
-    }
-    // Keep the whole batch's loads ahead of its compute (the scheduler would
-    // otherwise interleave them to save registers, serialising the latency).
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](const WB& w, const V8 (&xb)[D][4][MT]) {
     f32x4 cs[MT];
 #pragma unroll
-    for (int d = 0; d < NB; ++d)
+    for (int d = 0; d < D; ++d)
 #pragma unroll
       for (int gg = 0; gg < GPT; ++gg) {
-        const int p = d * GPT + gg, slot = p & 3;
+        const int pg = d * GPT + gg, slot = pg & 3;
         f32x4 cm[MT][NTW];
 #pragma unroll
         for (int b = 0; b < BPG; ++b) {
-          const int w = gg * BPG + b;
+          const int kw = gg * BPG + b;
 #pragma unroll
           for (int j = 0; j < NTW; ++j) {
-            const V8 a = biased_word<DT>(q[d][j][w], kMask, kMagic);
+            const V8 a = biased_word<DT>(w.q[d][j][kw], kMask, kMagic);
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) cm[mt][j] = mfma16x16x32(a, xb[d][w][mt], b == 0 ? zero4 : cm[mt][j]);
+            for (int mt = 0; mt < MT; ++mt) cm[mt][j] = mfma16x16x32(a, xb[d][kw][mt], b == 0 ? zero4 : cm[mt][j]);
           }
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            cs[mt] = mfma16x16x32(sel[slot], xb[d][w][mt], (slot == 0 && b == 0) ? zero4 : cs[mt]);
+            cs[mt] = mfma16x16x32(sel[slot], xb[d][kw][mt], (slot == 0 && b == 0) ? zero4 : cs[mt]);
         }
         // s * C onto the accumulator (output rows 4lg + r).
 #pragma unroll
         for (int j = 0; j < NTW; ++j)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float sr = (float)srow[d][j][gg][r];
+            const float sr = (float)w.srow[d][j][gg][r];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[mt][j][r] = __builtin_fmaf(sr, cm[mt][j][r], acc[mt][j][r]);
           }
-        if (slot == 3 || p == NGR - 1) {  // fold the block's -s (B + z) * sum(x) terms
+        if (slot == 3 || pg == NGR - 1) {  // fold the block's -s (B + z) * sum(x) terms
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x4f32(corrA[p >> 2][j], cs[mt][0], acc[mt][j]);
+            for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x4f32(w.corrA[pg >> 2][j], cs[mt][0], acc[mt][j]);
         }
       }
   };
+  // Everything a batch needs -- activation fragments first, then weights
+  // and scales -- is loaded one batch ahead; loads return in issue order, so
+  // waiting for batch b never waits for batch b + 1.
+  auto prefetch = [&](int bi, WB& w) {
+    if (last_masked && bi == nbatch - 1)
+      load_x(bi, w.xb, true);
+    else
+      load_x(bi, w.xb, false);
+    load_w(bi, w);
+  };
+  auto step = [&](int bi, const WB& cur, WB& next) {
+    if (bi + 1 < nbatch) prefetch(bi + 1, next);
+    // Keep the prefetch ahead of this batch's compute (the scheduler would
+    // otherwise interleave loads with math to save registers).
+    __builtin_amdgcn_sched_barrier(0);
+    compute(cur, cur.xb);
+  };
 
-  // Main loop: batches of D fully-valid tiles; remainder one tile at a time.
-  int i0 = 0;
-  for (; i0 + D <= nfull; i0 += D) run_batch(std::integral_constant<int, D>{}, i0, false);
-  for (int i = i0; i < niter; ++i) run_batch(std::integral_constant<int, 1>{}, i, i >= nfull);
+  if (nbatch > 0) {
+    WB wa, wb;
+    prefetch(0, wa);
+    for (int bi = 0; bi < nbatch; bi += 2) {
+      step(bi, wa, wb);
+      if (bi + 1 < nbatch) step(bi + 1, wb, wa);
+    }
+  }
 
   // Reduce the WK waves that share columns.
   if constexpr (WK > 1) {
@@ -279,7 +313,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __
 
   constexpr int QPR = NTG * 4;  // float4 quads per row of this column group
   const int64_t nbase = (int64_t)blockIdx.x * NTG * 16;
-  for (int idx = threadIdx.x; idx < M * QPR; idx += 256) {
+  for (int idx = threadIdx.x; idx < M * QPR; idx += NTHREADS) {
     const int m = idx / QPR;
     const int64_t n0 = nbase + 4 * (idx % QPR);
     if (n0 >= N) continue;
@@ -296,29 +330,35 @@ __global__ __launch_bounds__(256) void skinny_kernel(const typename DT::elem* __
 
 template <typename DT>
 hipError_t launch_skinny_dt_impl(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                            const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, hipStream_t s) {
+                                 const void* bias, void* out, const Geom& g, void* ws, int32_t* counters,
+                                 hipStream_t s) {
   using E = typename DT::elem;
   const uint16_t* sbase = (const uint16_t*)sr;
   const uint64_t* zbase = (const uint64_t*)zr;
   const int mt = (g.M + 15) / 16;
-  const int ntw = p.variant / 10, wk = p.variant % 10;
+  const int ntw = p.variant / 10000, wn = (p.variant / 100) % 100, wk = p.variant % 100;
   const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
   dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
-#define SGL_SKINNY(MT_, NTW_, WK_, GPT_)                                                                         \
-  if (mt == MT_ && ntw == NTW_ && wk == WK_ && gpt == GPT_) {                                                  \
-    hipLaunchKernelGGL((skinny_kernel<MT_, NTW_, WK_, GPT_, DT>), grid, dim3(256), 0, s, (const E*)x,          \
-                       (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters, (int)g.M,   \
-                       (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);            \
-    return hipGetLastError();                                                                                  \
+#define SGL_SKINNY(MT_, NTW_, WN_, WK_, GPT_)                                                                  \
+  if (mt == MT_ && ntw == NTW_ && wn == WN_ && wk == WK_ && gpt == GPT_) {                                   \
+    hipLaunchKernelGGL((skinny_kernel<MT_, NTW_, WN_, WK_, GPT_, DT>), grid, dim3(64 * WN_ * WK_), 0, s,     \
+                       (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws,       \
+                       counters, (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, \
+                       p.ks);                                                                                \
+    return hipGetLastError();                                                                                \
   }
-#define SGL_SKINNY_G(MT_, NTW_, WK_) SGL_SKINNY(MT_, NTW_, WK_, 1) SGL_SKINNY(MT_, NTW_, WK_, 2) SGL_SKINNY(MT_, NTW_, WK_, 4)
-#define SGL_SKINNY_MT(NTW_, WK_) SGL_SKINNY_G(1, NTW_, WK_) SGL_SKINNY_G(2, NTW_, WK_)
-  SGL_SKINNY_MT(1, 1)
-  SGL_SKINNY_MT(1, 2)
-  SGL_SKINNY_MT(1, 4)
-  SGL_SKINNY_MT(2, 1)
-  SGL_SKINNY_MT(2, 2)
-  SGL_SKINNY_MT(4, 1)
+#define SGL_SKINNY_G(MT_, NTW_, WN_, WK_) \
+  SGL_SKINNY(MT_, NTW_, WN_, WK_, 1) SGL_SKINNY(MT_, NTW_, WN_, WK_, 2) SGL_SKINNY(MT_, NTW_, WN_, WK_, 4)
+#define SGL_SKINNY_MT(NTW_, WN_, WK_) SGL_SKINNY_G(1, NTW_, WN_, WK_) SGL_SKINNY_G(2, NTW_, WN_, WK_)
+  SGL_SKINNY_MT(1, 1, 4)
+  SGL_SKINNY_MT(1, 1, 8)
+  SGL_SKINNY_MT(1, 1, 16)
+  SGL_SKINNY_MT(1, 2, 2)
+  SGL_SKINNY_MT(1, 4, 1)
+  SGL_SKINNY_MT(1, 4, 4)
+  SGL_SKINNY_MT(2, 2, 2)
+  SGL_SKINNY_MT(2, 4, 1)
+  SGL_SKINNY_MT(2, 2, 4)
 #undef SGL_SKINNY_MT
 #undef SGL_SKINNY_G
 #undef SGL_SKINNY
