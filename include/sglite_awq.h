@@ -102,6 +102,66 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype,
                    void* ws, int64_t ws_bytes, int32_t* counters, awq_stream_t stream);
 
+/* ---- grouped MoE -------------------------------------------------------------
+ * The stages of the fused MoE backend
+ * (python/sglite/srt/model_executor/layers/fused_moe/fused.py:101-202) with AWQ
+ * expert weights.  Experts are stacked: expert e's repacked weights, scales
+ * and zeros (awq_repack_cdna4 of that expert) start at e times the strides
+ * awq_moe_expert_strides reports (each buffer's per-expert size rounded up to
+ * 256 bytes).  A routed row is r = t * topk + j (token t, slot j). */
+
+int awq_moe_expert_strides(int64_t K, int64_t N, int64_t G, int64_t* w_stride, int64_t* s_stride,
+                           int64_t* z_stride);
+
+/* softmax(gating_output[T, E]) -> top-k -> optionally w / (sum(w) + 1e-8);
+ * replaces sgl_kernel.topk_softmax and the renormalisation of fused.py:11-31.
+ * Ties go to the lower expert index.  E <= 512, 1 <= topk <= min(E, 64). */
+int awq_moe_topk_softmax(const float* gating_output, float* topk_weights, int32_t* topk_ids, int64_t T,
+                         int64_t E, int64_t topk, int renormalize, awq_stream_t stream);
+
+/* Sorts the routed rows by expert (stable) and pads each expert's bucket to a
+ * multiple of block_size with the sentinel numel; replaces
+ * moe_align_block_size (fused.py:34-61, sgl_kernel's align kernel).
+ *   sorted_ids[awq_moe_sorted_capacity(numel, E, block_size)]
+ *   expert_ids[awq_moe_block_capacity(numel, E, block_size)]  (-1 past the end)
+ *   num_tokens_post_pad[1], expert_offsets[E + 1] (padded bucket starts)
+ * Ids outside [0, E) are dropped.  block_size % 16 == 0, E <= 512,
+ * numel < 2^24. */
+int64_t awq_moe_sorted_capacity(int64_t numel, int64_t E, int64_t block_size);
+int64_t awq_moe_block_capacity(int64_t numel, int64_t E, int64_t block_size);
+int awq_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_size,
+                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
+                             int32_t* expert_offsets, awq_stream_t stream);
+
+enum { AWQ_MOE_ACT_NONE = 0, AWQ_MOE_ACT_SILU = 1, AWQ_MOE_ACT_GELU = 2 };
+
+/* Grouped W4A16 GEMM over the expert buckets; replaces fused_moe_kernel
+ * (python/sglite/kernels/triton/fused_moe.py:54-183, launched by
+ * python/sglite/kernels/moe_triton.py:8-65) for AWQ B operands.
+ *   a        [a_rows, K]; routed row r reads activation row r / top_k
+ *            (top_k = topk for the first GEMM, 1 for the second, as in
+ *            moe_triton.py's `top_k` argument)
+ *   w/s/z    expert-stacked repacked weights of [K, N] per expert
+ *   out      activation == AWQ_MOE_ACT_NONE: [num_routed, N], row r
+ *            activation != NONE: N = 2I (gate columns first, then up), the
+ *            gate/up outputs are rounded and combined as
+ *            act(gate) * up -> [num_routed, I] (silu_and_mul / gelu_and_mul of
+ *            python/sglite/srt/model_executor/layers/activation.py:11-23);
+ *            needs I % 16 == 0
+ *   mul_routed_weight: multiply by topk_weights[r] (fp32) before the cast
+ *            (MUL_ROUTED_WEIGHT, triton/fused_moe.py:174-178)
+ * Rows of padding (id >= num_routed) are skipped. */
+int awq_moe_w4a16_gemm(const void* a, int64_t a_rows, const void* w, const void* s, const void* z, int64_t E,
+                       int64_t N, int64_t K, int64_t G, int dtype, const int32_t* sorted_ids, int64_t sorted_cap,
+                       const int32_t* expert_offsets, const float* topk_weights, int64_t num_routed, int64_t top_k,
+                       int activation, int mul_routed_weight, void* out, awq_stream_t stream);
+
+/* out[t, :] = rnd(sum_j in[t, j, :]) with an fp32 sum; replaces
+ * moe_sum_reduce_triton (python/sglite/kernels/moe_triton.py:68-102).
+ * H % 8 == 0; in and out 16-byte aligned. */
+int awq_moe_sum_reduce(const void* in, void* out, int64_t T, int64_t topk, int64_t H, int dtype,
+                       awq_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

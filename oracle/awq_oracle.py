@@ -269,38 +269,104 @@ def silu_and_mul(h: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.silu(hf[..., :d]) * hf[..., d:]
 
 
+def gelu_and_mul(h: torch.Tensor) -> torch.Tensor:
+    """gelu(h[..., :d]) * h[..., d:] in fp32 with the erf form of GELU (activation.py:18-23)."""
+    d = h.shape[-1] // 2
+    hf = h.float()
+    return torch.nn.functional.gelu(hf[..., :d]) * hf[..., d:]
+
+
+_ACT = {"silu": silu_and_mul, "gelu": gelu_and_mul}
+
+
+def moe_align_block_size(topk_ids, block_size: int, num_experts: int):
+    """Stable counting sort of the routed rows by expert (fused.py:34-61).
+
+    Returns ``(sorted_ids, expert_ids, num_tokens_post_pad, offsets)`` as numpy
+    int32 arrays: expert e's rows occupy ``sorted_ids[offsets[e]:offsets[e+1]]``
+    in increasing row order, padded to a multiple of ``block_size`` with the
+    sentinel ``n = topk_ids.size``; ``expert_ids[b]`` is the expert of block b
+    (-1 past the last block).  Ids outside ``[0, num_experts)`` are dropped.
+    The sgl_kernel layout is not observable through the MoE output (rows are
+    independent), so its bucket order is this build's choice: stable."""
+    ids = np.asarray(topk_ids).reshape(-1).astype(np.int64)
+    n = ids.size
+    cap = n + num_experts * (block_size - 1)
+    bcap = (cap + block_size - 1) // block_size
+    sorted_ids = np.full(cap, -7, dtype=np.int32)  # -7: never written (not read by consumers)
+    expert_ids = np.full(bcap, -1, dtype=np.int32)
+    offsets = np.zeros(num_experts + 1, dtype=np.int32)
+    pos = 0
+    for e in range(num_experts):
+        rows = np.nonzero(ids == e)[0]
+        offsets[e] = pos
+        sorted_ids[pos:pos + rows.size] = rows
+        padded = -(-rows.size // block_size) * block_size
+        sorted_ids[pos + rows.size:pos + padded] = n
+        expert_ids[pos // block_size:(pos + padded) // block_size] = e
+        pos += padded
+    offsets[num_experts] = pos
+    return sorted_ids, expert_ids, np.array([pos], dtype=np.int32), offsets
+
+
+def moe_grouped_gemm(a: torch.Tensor, w: Dict[str, torch.Tensor], topk_weights: Optional[torch.Tensor],
+                     topk_ids: torch.Tensor, top_k: int, group_size: int, activation: Optional[str] = None,
+                     mul_routed_weight: bool = False) -> torch.Tensor:
+    """One grouped GEMM of the MoE path per routed row r = t * topk + j
+    (triton/fused_moe.py:54-183): ``a[r // top_k] @ W[expert(r)]`` in fp32,
+    times ``topk_weights[r]`` when ``mul_routed_weight``, cast to a's dtype;
+    with an ``activation`` the cast output's gate/up halves are combined as
+    act(gate) * up in fp32 and cast again (activation.py:11-23).
+    ``w`` holds expert-stacked ``qweight``/``qzeros``/``scales``."""
+    dt = a.dtype
+    ids = topk_ids.reshape(-1).cpu().long()
+    n = ids.numel()
+    af = a.detach().cpu().float()
+    tw = None if topk_weights is None else topk_weights.reshape(-1).cpu().float()
+    N = w["qweight"].shape[2] * 8
+    out = torch.zeros((n, N // 2 if activation else N), dtype=dt)
+    for e in torch.unique(ids).tolist():
+        if e < 0 or e >= w["qweight"].shape[0]:
+            continue
+        rows = torch.nonzero(ids == e, as_tuple=True)[0]
+        W = dequantize(w["qweight"][e], w["qzeros"][e], w["scales"][e], group_size).float()
+        y = af[rows // top_k] @ W
+        if mul_routed_weight:
+            y = y * tw[rows][:, None]
+        y = y.to(dt)
+        if activation:
+            y = _ACT[activation](y).to(dt)
+        out[rows] = y
+    return out
+
+
 def fused_moe_awq(x: torch.Tensor, w1: Dict[str, torch.Tensor], w2: Dict[str, torch.Tensor],
-                  topk_weights: torch.Tensor, topk_ids: torch.Tensor, group_size: int) -> torch.Tensor:
+                  topk_weights: torch.Tensor, topk_ids: torch.Tensor, group_size: int, activation: str = "silu",
+                  apply_router_weight_on_input: bool = False, group_size2: Optional[int] = None) -> torch.Tensor:
     """Grouped AWQ MoE following fused.py:101-202 and triton/fused_moe.py:7-50, 174-178.
 
-    GEMM1 per (token, slot) in fp32, cast to the activation dtype; silu_and_mul
+    GEMM1 per (token, slot) in fp32 (times the routed weight when it is
+    applied on the input), cast to the activation dtype; act_and_mul
     (computed in fp32, cast); GEMM2 in fp32 times the routed weight (fp32)
-    before the cast; the top-k outputs are summed in fp32 and cast.
+    before the cast otherwise; the top-k outputs are summed in fp32 and cast.
     ``w1``/``w2`` hold expert-stacked ``qweight``/``qzeros``/``scales``.
     """
     dt = x.dtype
     T, H = x.shape
-    E = w1["qweight"].shape[0]
     k = topk_ids.shape[1]
-    W1 = [dequantize(w1["qweight"][e], w1["qzeros"][e], w1["scales"][e], group_size).float() for e in range(E)]
-    W2 = [dequantize(w2["qweight"][e], w2["qzeros"][e], w2["scales"][e], group_size).float() for e in range(E)]
-    xf = x.detach().cpu().float()
-    out = torch.zeros((T, W2[0].shape[1]), dtype=torch.float32)
-    ids = topk_ids.cpu().long()
-    tw = topk_weights.cpu().float()
-    for e in range(E):
-        rows, slots = torch.nonzero(ids == e, as_tuple=True)
-        if rows.numel() == 0:
-            continue
-        h1 = (xf[rows] @ W1[e]).to(dt)
-        h2 = silu_and_mul(h1).to(dt)
-        y = (h2.float() @ W2[e]) * tw[rows, slots][:, None]
-        out.index_put_((rows,), y.to(dt).float(), accumulate=True)
-    return out.to(dt)
+    g2 = group_size if group_size2 is None else group_size2
+    h2 = moe_grouped_gemm(x, w1, topk_weights, topk_ids, k, group_size, activation, apply_router_weight_on_input)
+    y = moe_grouped_gemm(h2, w2, topk_weights, topk_ids, 1, g2, None, not apply_router_weight_on_input)
+    return moe_sum_reduce(y.view(T, k, -1))
+
+
+def moe_sum_reduce(y: torch.Tensor) -> torch.Tensor:
+    """out[t] = rnd(sum_j y[t, j]) with an fp32 sum (triton/fused_moe.py:7-50)."""
+    return y.float().sum(dim=1).to(y.dtype)
 
 
 def fused_moe_awq_loops(x, w1, w2, topk_weights, topk_ids, group_size) -> torch.Tensor:
-    """Explicit per-(token, slot) loop form of :func:`fused_moe_awq` (tiny shapes only)."""
+    """Explicit per-(token, slot) loop form of :func:`fused_moe_awq` (silu, tiny shapes only)."""
     dt = x.dtype
     T, H = x.shape
     k = topk_ids.shape[1]

@@ -41,7 +41,20 @@ SIGNATURES = {
     "awq_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "awq_counter_bytes": (_i64, [_i64]),
     "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp]),
+    "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                      ctypes.POINTER(_i64)]),
+    "awq_moe_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "awq_moe_sorted_capacity": (_i64, [_i64, _i64, _i64]),
+    "awq_moe_block_capacity": (_i64, [_i64, _i64, _i64]),
+    "awq_moe_align_block_size": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "awq_moe_w4a16_gemm": (_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp, _i64,
+                                  _i64, _int, _int, _vp, _vp]),
+    "awq_moe_sum_reduce": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp]),
 }
+
+AWQ_MOE_ACT_NONE = 0
+AWQ_MOE_ACT_SILU = 1
+AWQ_MOE_ACT_GELU = 2
 
 _lib: Optional[ctypes.CDLL] = None
 

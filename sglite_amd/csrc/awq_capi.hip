@@ -195,4 +195,129 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
                     "awq_w4a16_gemm launch");
 }
 
+int64_t awq_moe_sorted_capacity(int64_t numel, int64_t E, int64_t block_size) {
+  if (numel < 0 || E <= 0 || block_size <= 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sorted_capacity: numel >= 0, E > 0, block_size > 0 required");
+  return moe_sorted_capacity(numel, E, block_size);
+}
+
+int64_t awq_moe_block_capacity(int64_t numel, int64_t E, int64_t block_size) {
+  if (numel < 0 || E <= 0 || block_size <= 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_block_capacity: numel >= 0, E > 0, block_size > 0 required");
+  return moe_block_capacity(numel, E, block_size);
+}
+
+int awq_moe_expert_strides(int64_t K, int64_t N, int64_t G, int64_t* w_stride, int64_t* s_stride,
+                           int64_t* z_stride) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (!w_stride || !s_stride || !z_stride)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_expert_strides: null pointer argument");
+  const MoeStrides m = moe_expert_strides(make_geom(0, N, K, Gr));
+  *w_stride = m.w;
+  *s_stride = m.s;
+  *z_stride = m.z;
+  return ok();
+}
+
+int awq_moe_topk_softmax(const float* gating_output, float* topk_weights, int32_t* topk_ids, int64_t T, int64_t E,
+                         int64_t topk, int renormalize, awq_stream_t stream) {
+  if (T < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_topk_softmax: T must be non-negative");
+  if (E <= 0 || E > 512) return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_topk_softmax: E must be in [1, 512], got %lld",
+                                     (long long)E);
+  if (topk < 1 || topk > E || topk > 64)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_topk_softmax: topk must be in [1, min(E, 64)], got %lld",
+                (long long)topk);
+  if (T > (int64_t(1) << 24)) return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_topk_softmax: T must be below 2^24");
+  if (T == 0) return ok();
+  if (!gating_output || !topk_weights || !topk_ids)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_topk_softmax: null pointer argument");
+  return hip_status(launch_moe_topk(gating_output, topk_weights, topk_ids, T, E, topk, renormalize ? 1 : 0,
+                                    (hipStream_t)stream),
+                    "awq_moe_topk_softmax launch");
+}
+
+int awq_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_size,
+                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
+                             int32_t* expert_offsets, awq_stream_t stream) {
+  if (E <= 0 || E > 512)
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_align_block_size: E must be in [1, 512], got %lld", (long long)E);
+  if (block_size <= 0 || block_size % 16 != 0 || block_size > 1024)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "awq_moe_align_block_size: block_size must be a positive multiple of 16 up to 1024, got %lld",
+                (long long)block_size);
+  if (numel < 0 || numel >= (int64_t(1) << 24))
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_align_block_size: numel must be in [0, 2^24), got %lld",
+                (long long)numel);
+  if ((numel > 0 && !topk_ids) || !sorted_ids || !expert_ids || !num_tokens_post_pad || !expert_offsets)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_align_block_size: null pointer argument");
+  return hip_status(launch_moe_align(topk_ids, numel, E, block_size, sorted_ids, expert_ids, num_tokens_post_pad,
+                                     expert_offsets, (hipStream_t)stream),
+                    "awq_moe_align_block_size launch");
+}
+
+int awq_moe_w4a16_gemm(const void* a, int64_t a_rows, const void* w, const void* s, const void* z, int64_t E,
+                       int64_t N, int64_t K, int64_t G, int dtype, const int32_t* sorted_ids, int64_t sorted_cap,
+                       const int32_t* expert_offsets, const float* topk_weights, int64_t num_routed, int64_t top_k,
+                       int activation, int mul_routed_weight, void* out, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (E <= 0 || E > 512)
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_w4a16_gemm: E must be in [1, 512], got %lld", (long long)E);
+  if (activation != AWQ_MOE_ACT_NONE && activation != AWQ_MOE_ACT_SILU && activation != AWQ_MOE_ACT_GELU)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_w4a16_gemm: unknown activation %d", activation);
+  if (activation != AWQ_MOE_ACT_NONE && N % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "awq_moe_w4a16_gemm: gate/up pairing needs N = 2I with I %% 16 == 0, got N=%lld", (long long)N);
+  if (top_k <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_w4a16_gemm: top_k must be positive");
+  if (num_routed < 0 || num_routed >= (int64_t(1) << 24) || sorted_cap < 0 || sorted_cap >= (int64_t(1) << 30))
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_w4a16_gemm: num_routed must be below 2^24 and sorted_cap below 2^30");
+  if ((num_routed + top_k - 1) / top_k > a_rows)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "awq_moe_w4a16_gemm: %lld routed rows with top_k %lld need %lld activation rows, a has %lld",
+                (long long)num_routed, (long long)top_k, (long long)((num_routed + top_k - 1) / top_k),
+                (long long)a_rows);
+  if (num_routed == 0 || sorted_cap == 0) return ok();
+  if (!a || !w || !s || !z || !sorted_ids || !expert_offsets || !out || (mul_routed_weight && !topk_weights))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_w4a16_gemm: null pointer argument");
+  if (!aligned(a, 16) || !aligned(out, 8) || !aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "awq_moe_w4a16_gemm: a, w, s, z must be 16-byte aligned and out 8-byte aligned");
+  MoeGemmParams p{};
+  p.x = a;
+  p.w = w;
+  p.s = s;
+  p.z = z;
+  p.sorted = sorted_ids;
+  p.offsets = expert_offsets;
+  p.topk_w = topk_weights;
+  p.out = out;
+  p.E = E;
+  p.a_div = top_k;
+  p.num_routed = num_routed;
+  p.sorted_cap = sorted_cap;
+  p.g = make_geom(0, N, K, Gr);
+  p.epi = activation;
+  p.mul_rw = mul_routed_weight ? 1 : 0;
+  p.dtype = dtype;
+  return hip_status(launch_moe_gemm(p, (hipStream_t)stream), "awq_moe_w4a16_gemm launch");
+}
+
+int awq_moe_sum_reduce(const void* in, void* out, int64_t T, int64_t topk, int64_t H, int dtype,
+                       awq_stream_t stream) {
+  if (dtype != AWQ_DTYPE_FP16 && dtype != AWQ_DTYPE_BF16)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sum_reduce: dtype must be 0 or 1, got %d", dtype);
+  if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sum_reduce: T >= 0, topk > 0 and H %% 8 == 0 required");
+  if (T * H >= (int64_t(1) << 34) || topk > 1024)
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_sum_reduce: problem too large");
+  if (T == 0) return ok();
+  if (!in || !out) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sum_reduce: null pointer argument");
+  if (!aligned(in, 16) || !aligned(out, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sum_reduce: in and out must be 16-byte aligned");
+  return hip_status(launch_moe_sum(in, out, T, topk, H, dtype, (hipStream_t)stream), "awq_moe_sum_reduce launch");
+}
+
 }  // extern "C"

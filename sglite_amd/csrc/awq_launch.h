@@ -41,4 +41,35 @@ hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const vo
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);
 
+// Grouped MoE path (awq_moe.hip).
+// Byte strides between consecutive experts' repacked weights, scales, zeros.
+struct MoeStrides {
+  int64_t w, s, z;
+};
+MoeStrides moe_expert_strides(const Geom& g);
+int64_t moe_sorted_capacity(int64_t n, int64_t E, int64_t bs);
+int64_t moe_block_capacity(int64_t n, int64_t E, int64_t bs);
+hipError_t launch_moe_topk(const float* logits, float* tw, int32_t* tid, int64_t T, int64_t E, int64_t k, int renorm,
+                           hipStream_t s);
+hipError_t launch_moe_align(const int32_t* ids, int64_t n, int64_t E, int64_t bs, int32_t* sorted, int32_t* expert_ids,
+                            int32_t* num_post_pad, int32_t* offsets, hipStream_t s);
+
+struct MoeGemmParams {
+  const void* x;           // activation rows
+  const void* w;           // expert-stacked repacked weights / scales / zeros
+  const void* s;
+  const void* z;
+  const int32_t* sorted;   // from launch_moe_align
+  const int32_t* offsets;  // padded bucket offsets [E + 1]
+  const float* topk_w;     // routed weights [num_routed]
+  void* out;
+  int64_t E, a_div, num_routed, sorted_cap;
+  Geom g;       // per-expert geometry (M unused)
+  int epi;      // 0 plain, 1 silu_and_mul, 2 gelu_and_mul (gate/up pairing)
+  int mul_rw;   // multiply by the routed weight before the cast
+  int dtype;
+};
+hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s);
+hipError_t launch_moe_sum(const void* in, void* out, int64_t T, int64_t k, int64_t H, int dtype, hipStream_t s);
+
 }  // namespace sgl_awq

@@ -9,6 +9,7 @@ allocates only through torch's caching allocator, so it can be captured in a
 
 from __future__ import annotations
 
+import ctypes
 from typing import NamedTuple, Optional, Tuple
 
 import torch
@@ -179,4 +180,151 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
     _lib.check(lib.awq_w4a16_gemm(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
                                   out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _ptr(ws), wsb, _ptr(counters),
                                   _stream(dev)), "awq_w4a16_gemm")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Grouped MoE (experts stacked on dim 0).
+# ---------------------------------------------------------------------------
+
+class RepackedExperts(NamedTuple):
+    """Expert-stacked repacked tensors, one row per expert (rows padded to
+    256 bytes); ``expert(e)`` views expert e's linear as a ``Repacked``."""
+    w: torch.Tensor  # int32 [E, w_stride / 4]
+    s: torch.Tensor  # scale dtype [E, s_stride / 2]
+    z: torch.Tensor  # int64 [E, z_stride / 8]
+    K: int
+    N: int
+    G: int
+
+    def expert(self, e: int) -> Repacked:
+        NT, NG = (self.N + 15) // 16, self.K // self.G
+        return Repacked(self.w[e, :NT * ((self.K + 127) // 128) * 256], self.s[e, :NT * NG * 16].view(NT, NG, 16),
+                        self.z[e, :NT * NG].view(NT, NG))
+
+
+def expert_strides(K: int, N: int, group_size: int) -> Tuple[int, int, int]:
+    """Byte strides between consecutive experts' weights, scales and zero words."""
+    G = resolve_group_size(group_size, K)
+    w, s, z = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(_lib.load().awq_moe_expert_strides(K, N, G, ctypes.byref(w), ctypes.byref(s), ctypes.byref(z)),
+               "awq_moe_expert_strides")
+    return w.value, s.value, z.value
+
+
+def repack_experts(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> RepackedExperts:
+    """AWQ expert stacks ``[E, K, N/8]`` / ``[E, K/G, N/8]`` / ``[E, K/G, N]`` -> stacked tile layout.
+
+    Each expert is repacked into its own row of the stacks (the layout
+    ``awq_moe_w4a16_gemm`` expects)."""
+    _require_cuda(qweight, qzeros, scales)
+    if qweight.dim() != 3 or qzeros.dim() != 3 or scales.dim() != 3:
+        raise ValueError("expert stacks must be 3-D [E, ...]")
+    E = qweight.shape[0]
+    if qzeros.shape[0] != E or scales.shape[0] != E:
+        raise ValueError("qweight, qzeros and scales must stack the same number of experts")
+    K, N, G = _check_awq_shapes(qweight[0], qzeros[0], scales[0])
+    code = dtype_code(scales.dtype)
+    ws, ss, zs = expert_strides(K, N, G)
+    dev = qweight.device
+    w = torch.empty((E, ws // 4), dtype=torch.int32, device=dev)
+    s = torch.zeros((E, ss // 2), dtype=scales.dtype, device=dev)
+    z = torch.zeros((E, zs // 8), dtype=torch.int64, device=dev)
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    lib = _lib.load()
+    st = _stream(dev)
+    for e in range(E):
+        _lib.check(lib.awq_repack_cdna4(qweight[e].data_ptr(), qzeros[e].data_ptr(), scales[e].data_ptr(), code, K, N, G,
+                                        w[e].data_ptr(), s[e].data_ptr(), z[e].data_ptr(), st), "awq_repack_cdna4")
+    return RepackedExperts(w, s, z, K, N, G)
+
+
+def moe_topk_softmax(gating_output: torch.Tensor, topk: int, renormalize: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """softmax(fp32 logits) -> top-k -> optional ``w / (sum(w) + 1e-8)``; (weights fp32, ids int32)."""
+    _require_cuda(gating_output)
+    if gating_output.dim() != 2:
+        raise ValueError("gating_output must be [T, E]")
+    logits = _aligned(gating_output.float(), 4)
+    T, E = logits.shape
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.load().awq_moe_topk_softmax(logits.data_ptr(), w.data_ptr(), ids.data_ptr(), T, E, topk,
+                                                1 if renormalize else 0, _stream(logits.device)),
+               "awq_moe_topk_softmax")
+    return w, ids
+
+
+class MoeAlignment(NamedTuple):
+    sorted_ids: torch.Tensor          # int32 [sorted capacity]
+    expert_ids: torch.Tensor          # int32 [block capacity]
+    num_tokens_post_pad: torch.Tensor  # int32 [1]
+    expert_offsets: torch.Tensor      # int32 [E + 1]
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int) -> MoeAlignment:
+    """Stable sort of the routed rows by expert, buckets padded to ``block_size`` (sentinel ``topk_ids.numel()``)."""
+    _require_cuda(topk_ids)
+    if topk_ids.dtype != torch.int32:
+        raise ValueError("topk_ids must be int32")
+    ids = topk_ids.contiguous().reshape(-1)
+    n = ids.numel()
+    lib = _lib.load()
+    cap = _lib.check(lib.awq_moe_sorted_capacity(n, num_experts, block_size), "awq_moe_sorted_capacity")
+    bcap = _lib.check(lib.awq_moe_block_capacity(n, num_experts, block_size), "awq_moe_block_capacity")
+    dev = ids.device
+    sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(bcap, dtype=torch.int32, device=dev)
+    npp = torch.empty(1, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    _lib.check(lib.awq_moe_align_block_size(ids.data_ptr() if n else None, n, num_experts, block_size,
+                                            sorted_ids.data_ptr(), expert_ids.data_ptr(), npp.data_ptr(),
+                                            offsets.data_ptr(), _stream(dev)), "awq_moe_align_block_size")
+    return MoeAlignment(sorted_ids, expert_ids, npp, offsets)
+
+
+_ACT_CODE = {None: _lib.AWQ_MOE_ACT_NONE, "silu": _lib.AWQ_MOE_ACT_SILU, "gelu": _lib.AWQ_MOE_ACT_GELU}
+
+
+def moe_gemm(a: torch.Tensor, experts: RepackedExperts, K: int, N: int, group_size: int, align: MoeAlignment,
+             topk_weights: Optional[torch.Tensor], num_routed: int, top_k: int, activation: Optional[str] = None,
+             mul_routed_weight: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Grouped W4A16 GEMM over the expert buckets.
+
+    Routed row r reads ``a[r // top_k]``; the output has ``num_routed`` rows of
+    ``N`` columns, or ``N / 2`` with a gate/up ``activation`` ("silu"/"gelu")."""
+    _require_cuda(a, experts.w)
+    if a.dim() != 2 or a.shape[1] != K:
+        raise ValueError(f"a must be [rows, {K}], got {tuple(a.shape)}")
+    if a.dtype != experts.s.dtype:
+        raise ValueError(f"activation dtype {a.dtype} does not match the scale dtype {experts.s.dtype}")
+    if activation not in _ACT_CODE:
+        raise ValueError(f"unsupported activation {activation!r}")
+    G = resolve_group_size(group_size, K)
+    E = experts.w.shape[0]
+    ncols = N // 2 if activation is not None else N
+    a = _aligned(a)
+    if out is None:
+        out = torch.empty((num_routed, ncols), dtype=a.dtype, device=a.device)
+    if topk_weights is not None:
+        topk_weights = _aligned(topk_weights.float().reshape(-1), 4)
+    _lib.check(_lib.load().awq_moe_w4a16_gemm(
+        a.data_ptr(), a.shape[0], experts.w.data_ptr(), experts.s.data_ptr(), experts.z.data_ptr(), E, N, K, G,
+        dtype_code(a.dtype), align.sorted_ids.data_ptr(), align.sorted_ids.numel(), align.expert_offsets.data_ptr(),
+        _ptr(topk_weights), num_routed, top_k, _ACT_CODE[activation], 1 if mul_routed_weight else 0, out.data_ptr(),
+        _stream(a.device)), "awq_moe_w4a16_gemm")
+    return out
+
+
+def moe_sum_reduce(inp: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[t] = rnd(sum_j inp[t, j]) with an fp32 sum (inp [T, k, H], out [T, H])."""
+    _require_cuda(inp, out)
+    if inp.dim() != 3 or out.dim() != 2 or out.shape[0] != inp.shape[0] or out.shape[1] != inp.shape[2]:
+        raise ValueError(f"shapes do not match: in {tuple(inp.shape)}, out {tuple(out.shape)}")
+    if inp.dtype != out.dtype:
+        raise ValueError("in and out must share a dtype")
+    if not (inp.is_contiguous() and out.is_contiguous()):
+        raise ValueError("in and out must be contiguous")
+    T, k, H = inp.shape
+    _lib.check(_lib.load().awq_moe_sum_reduce(inp.data_ptr(), out.data_ptr(), T, k, H, dtype_code(inp.dtype),
+                                              _stream(inp.device)), "awq_moe_sum_reduce")
     return out

@@ -298,3 +298,69 @@ def test_load_quantization_config_sources(tmp_path):
         quantization_config = {"quant_method": "gptq", "bits": 4}
 
     assert load_quantization_config("nowhere", GPTQ()) is None
+
+
+# --------------------------------------------------------------------------
+# MoE entry points: validation happens before any GPU work
+# --------------------------------------------------------------------------
+
+def test_moe_capacity_queries():
+    lib = _lib.load()
+    assert lib.awq_moe_sorted_capacity(4096, 128, 16) == 4096 + 128 * 15
+    assert lib.awq_moe_block_capacity(4096, 128, 16) == (4096 + 128 * 15 + 15) // 16
+    assert lib.awq_moe_sorted_capacity(0, 1, 16) == 15
+    assert lib.awq_moe_sorted_capacity(-1, 4, 16) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+
+
+def test_moe_topk_validation():
+    lib = _lib.load()
+    assert lib.awq_moe_topk_softmax(None, None, None, 4, 1000, 8, 1, None) == _lib.AWQ_STATUS_UNSUPPORTED
+    assert lib.awq_moe_topk_softmax(None, None, None, 4, 8, 9, 1, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert "topk" in _lib.last_error()
+    assert lib.awq_moe_topk_softmax(None, None, None, 4, 8, 2, 1, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_moe_topk_softmax(None, None, None, 0, 8, 2, 1, None) == _lib.AWQ_STATUS_OK
+
+
+def test_moe_align_validation():
+    lib = _lib.load()
+    st = lib.awq_moe_align_block_size(None, 10, 8, 24, None, None, None, None, None)
+    assert st == _lib.AWQ_STATUS_INVALID_ARGUMENT and "block_size" in _lib.last_error()
+    assert lib.awq_moe_align_block_size(None, 10, 600, 16, None, None, None, None, None) == _lib.AWQ_STATUS_UNSUPPORTED
+    assert lib.awq_moe_align_block_size(None, 10, 8, 16, None, None, None, None, None) == \
+        _lib.AWQ_STATUS_INVALID_ARGUMENT
+
+
+def _moe_gemm_status(**kw):
+    a = dict(a=None, a_rows=4, w=None, s=None, z=None, E=8, N=256, K=256, G=128, dtype=0, sorted_ids=None,
+             sorted_cap=64, offsets=None, tw=None, num_routed=8, top_k=2, act=1, mul=0, out=None, stream=None)
+    a.update(kw)
+    return _lib.load().awq_moe_w4a16_gemm(*a.values())
+
+
+def test_moe_gemm_validation():
+    assert _moe_gemm_status(N=48) == _lib.AWQ_STATUS_INVALID_ARGUMENT  # gate/up pairing needs I % 16 == 0
+    assert "pairing" in _lib.last_error()
+    assert _moe_gemm_status(act=7) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert _moe_gemm_status(a_rows=3) == _lib.AWQ_STATUS_INVALID_ARGUMENT  # 8 routed rows / top_k 2 need 4 rows
+    assert "activation rows" in _lib.last_error()
+    assert _moe_gemm_status(G=48) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert _moe_gemm_status(E=0) == _lib.AWQ_STATUS_UNSUPPORTED
+    assert _moe_gemm_status(top_k=0) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert _moe_gemm_status() == _lib.AWQ_STATUS_INVALID_ARGUMENT  # null pointers
+    assert _moe_gemm_status(num_routed=0) == _lib.AWQ_STATUS_OK       # nothing routed: no launch
+
+
+def test_moe_sum_validation():
+    lib = _lib.load()
+    assert lib.awq_moe_sum_reduce(None, None, 4, 8, 12, 0, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_moe_sum_reduce(None, None, 4, 8, 16, 3, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_moe_sum_reduce(None, None, 0, 8, 16, 0, None) == _lib.AWQ_STATUS_OK
+    assert lib.awq_moe_sum_reduce(None, None, 4, 8, 16, 0, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+
+
+def test_moe_backend_registry():
+    from sglite_amd.moe import SUPPORTED_MOE_BACKENDS, AWQFusedMoe, create_moe_backend
+    assert isinstance(create_moe_backend("awq_fused"), AWQFusedMoe)
+    assert "awq_fused" in SUPPORTED_MOE_BACKENDS
+    with pytest.raises(ValueError):
+        create_moe_backend("nope")

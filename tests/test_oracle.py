@@ -9,6 +9,8 @@ text (awq_triton.py:53-62, 93-96, 119-120; marlin_utils.py:249-282, 336-347).
 
 import os
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -312,6 +314,74 @@ def test_moe_vectorised_matches_loops():
     b = oracle.fused_moe_awq_loops(x, W1, W2, tw, ids, G)
     # same rounding points; only fp32 summation order differs
     torch.testing.assert_close(a.float(), b.float(), rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("n,E,bs", [(0, 4, 16), (7, 4, 16), (200, 8, 16), (4096, 128, 16), (333, 60, 32),
+                                    (50, 512, 64)])
+def test_moe_align_invariants(n, E, bs):
+    """Each bucket holds exactly its expert's rows in increasing order, then
+    sentinels up to a multiple of the block size; ids outside [0, E) vanish."""
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(-1, E, size=n).astype(np.int32)
+    sorted_ids, expert_ids, npp, off = oracle.moe_align_block_size(ids, bs, E)
+    assert sorted_ids.size == n + E * (bs - 1)
+    assert off[0] == 0 and off[E] == npp[0]
+    seen = []
+    for e in range(E):
+        bucket = sorted_ids[off[e]:off[e + 1]]
+        rows = np.nonzero(ids == e)[0]
+        assert (off[e + 1] - off[e]) % bs == 0
+        assert off[e + 1] - off[e] - rows.size < bs
+        np.testing.assert_array_equal(bucket[:rows.size], rows)
+        assert (bucket[rows.size:] == n).all()
+        assert (expert_ids[off[e] // bs:off[e + 1] // bs] == e).all()
+        seen.extend(rows.tolist())
+    assert sorted(seen) == np.nonzero((ids >= 0) & (ids < E))[0].tolist()
+    assert (expert_ids[npp[0] // bs:] == -1).all()
+
+
+def test_gelu_and_mul_closed_form():
+    h = torch.tensor([[-3.0, -0.5, 0.0, 2.0, 1.5, -2.0, 4.0, 0.25]])
+    ref = [0.5 * g * (1 + math.erf(g / math.sqrt(2))) * u for g, u in zip(h[0, :4].tolist(), h[0, 4:].tolist())]
+    # 1 + erf(x) cancels for x << 0, so the fp32 result carries an absolute error
+    torch.testing.assert_close(oracle.gelu_and_mul(h)[0], torch.tensor(ref), rtol=1e-6, atol=2e-6)
+    ref_s = [g / (1 + math.exp(-g)) * u for g, u in zip(h[0, :4].tolist(), h[0, 4:].tolist())]
+    torch.testing.assert_close(oracle.silu_and_mul(h)[0], torch.tensor(ref_s), rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("activation", [None, "silu", "gelu"])
+@pytest.mark.parametrize("mul", [False, True])
+def test_moe_grouped_gemm_matches_row_loops(activation, mul):
+    """Per routed row: a[r // top_k] @ W[e(r)] in float64, x weight, rounded; the
+    activation in float64 of the rounded halves."""
+    x, W1, W2, tw, ids, G = _moe_case(T=6, E=4, k=3)
+    k = ids.shape[1]
+    out = oracle.moe_grouped_gemm(x, W1, tw, ids, k, G, activation, mul)
+    for r in range(ids.numel()):
+        e = int(ids.reshape(-1)[r])
+        W = oracle.dequantize(W1["qweight"][e], W1["qzeros"][e], W1["scales"][e], G).double()
+        y = x[r // k].double() @ W
+        if mul:
+            y = y * float(tw.reshape(-1)[r])
+        y = y.half().double()
+        if activation:
+            d = y.shape[0] // 2
+            g, u = y[:d], y[d:]
+            a = g / (1 + torch.exp(-g)) if activation == "silu" else 0.5 * g * (1 + torch.erf(g / math.sqrt(2)))
+            y = (a * u).half().double()
+        torch.testing.assert_close(out[r].double(), y, rtol=2e-3, atol=2e-3)
+
+
+def test_moe_router_weight_on_input_moves_the_multiply():
+    x, W1, W2, _, ids, G = _moe_case(T=4, E=3, k=1)
+    # top-1 weights without renormalisation (renormalised they would all be 1)
+    tw = torch.rand(ids.shape, generator=torch.Generator().manual_seed(3)) * 0.5 + 0.25
+    a = oracle.fused_moe_awq(x, W1, W2, tw, ids, G, apply_router_weight_on_input=True)
+    h = oracle.moe_grouped_gemm(x, W1, tw, ids, 1, G, "silu", True)
+    y = oracle.moe_grouped_gemm(h, W2, None, ids, 1, G, None, False)
+    assert torch.equal(a, y.view(4, 1, -1).float().sum(1).half())
+    b = oracle.fused_moe_awq(x, W1, W2, tw, ids, G)
+    assert not torch.equal(a, b)
 
 
 # --------------------------------------------------------------------------
