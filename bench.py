@@ -98,6 +98,85 @@ def time_replays(graphs, n: int) -> float:
     return a.elapsed_time(b)
 
 
+def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, reps: int = 50) -> dict:
+    """Qwen3-30B-A3B-shaped experts: E=128, H=2048, I=768, top-8 of softmax(N(0,1) logits), T=512.
+
+    One forward = routing, alignment, grouped gate_up GEMM with silu_and_mul,
+    grouped down GEMM with the routed weight, top-k combine; replayed as one
+    HIP graph over `copies` distinct expert stacks (314 MB each, past the
+    Infinity Cache).  Algorithmic bytes: all experts' int4 weights, zeros and
+    fp16 scales, plus 2 bytes per element of each routed row's activation
+    traffic (x row, gate_up output, activation output, down output)."""
+    from sglite_amd.moe import fused_experts_impl, fused_topk, process_awq_moe_weights
+
+    E, H, I, k, T = 128, 2048, 768, 8, 512
+
+    def stack(K, N):
+        q = torch.randint(0, 16, (E, K, N), generator=gen, device=dev, dtype=torch.int32)
+        qw = pack_awq_gpu(q.view(E * K, N)).view(E, K, N // 8)
+        del q
+        z = torch.randint(0, 16, (E * (K // G), N), generator=gen, device=dev, dtype=torch.int32)
+        qz = pack_awq_gpu(z).view(E, K // G, N // 8)
+        s = (torch.rand((E, K // G, N), generator=gen, device=dev) * 0.018 + 0.002).to(torch.float16)
+        w = process_awq_moe_weights(qw, qz, s)
+        del qw, qz, s
+        return w
+
+    stacks = [(stack(H, 2 * I), stack(I, H)) for _ in range(copies)]
+    xg = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((T, H), generator=xg, device=dev).to(torch.float16)
+    logits = torch.randn((T, E), generator=xg, device=dev)
+    buf = x.clone()
+
+    def forward(c):
+        w1, w2 = stacks[c]
+
+        def f():
+            tw, ids = fused_topk(buf, logits, k, True)
+            fused_experts_impl(buf, w1, w2, tw, ids, "silu")
+        return f
+
+    graphs = [graph_of(forward(c)) for c in range(copies)]
+    time_replays(graphs, 10)
+    us = time_replays(graphs, reps) * 1e3 / reps
+
+    # Per-kernel durations: graphs of `copies` back-to-back launches of one stage.
+    tw, ids = fused_topk(x, logits, k, True)
+    align = ops.moe_align_block_size(ids, 16, E)
+    h = ops.moe_gemm(x, stacks[0][0].experts, H, 2 * I, G, align, tw, T * k, k, "silu", False)
+    y = ops.moe_gemm(h, stacks[0][1].experts, I, H, G, align, tw, T * k, 1, None, True)
+    stages = {
+        "topk_softmax": lambda c: ops.moe_topk_softmax(logits, k, True),
+        "align": lambda c: ops.moe_align_block_size(ids, 16, E),
+        "gate_up_silu": lambda c: ops.moe_gemm(x, stacks[c][0].experts, H, 2 * I, G, align, tw, T * k, k, "silu",
+                                               False, out=h),
+        "down_routed": lambda c: ops.moe_gemm(h, stacks[c][1].experts, I, H, G, align, tw, T * k, 1, None, True,
+                                              out=y),
+        "sum_reduce": lambda c: ops.moe_sum_reduce(y.view(T, k, H), buf),
+    }
+    kern = {}
+    for name, fn in stages.items():
+        g = graph_of(lambda fn=fn: [fn(c) for c in range(copies)])
+        time_replays([g], 3)
+        kern[name] = round(time_replays([g], 10) * 1e3 / (10 * copies), 2)
+        del g
+
+    def wbytes(K, N):
+        return E * (K * N // 2 + (K // G) * N // 2 + (K // G) * N * 2)
+
+    weights = wbytes(H, 2 * I) + wbytes(I, H)
+    act = T * k * (H + 2 * I + I + H) * 2
+    flops = 2 * T * k * (H * 2 * I + I * H)
+    gemm_us = kern["gate_up_silu"] + kern["down_routed"]
+    return {"workload": "Qwen3-30B-A3B-shaped MoE experts: E=128, H=2048, I=768, top-8, T=512, int4 group 128 "
+                        "with zero points, fp16; routing from softmax(N(0,1) logits)",
+            "us": round(us, 2), "GB/s": round((weights + act) / us / 1e3, 1),
+            "frac": round((weights + act) / us / 1e3 / HBM_PEAK_GBS, 4),
+            "TFLOP/s": round(flops / us / 1e6, 1), "algorithmic_bytes": weights + act, "flops": flops,
+            "gemm_GB/s": round((weights + act) / gemm_us / 1e3, 1), "kernels_us": kern,
+            "kernel": "moe_gemm_kernel (grouped W4A16)", "copies": copies}
+
+
 def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 30) -> dict:
     """The CPU oracle on the same layer, repeated until about ``min_seconds`` of work."""
     from oracle import awq_oracle as oracle
@@ -184,6 +263,7 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=36, help="distinct weight copies rotated through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--rocprof-summary", metavar="TRACE_DIR",
                     help="print a markdown summary of a rocprofv3 --kernel-trace run of this script and exit")
     ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
@@ -290,6 +370,8 @@ def main() -> int:
                    "peak": MFMA_FP16_PEAK_TFLOPS, "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
                    "kernel": "tiled_kernel", "linears": lin}
 
+    moe = None if args.no_moe else moe_bench(ops, dev, gen)
+
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
     line = {
@@ -313,6 +395,7 @@ def main() -> int:
         "roofline": roofline,
         "per_m": per_m,
         "prefill": prefill,
+        "moe": moe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -53,6 +53,7 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
 // Group-dependent dequantisation constants of one lane's column.
 struct ZS16 {
   f16x2 zb;  // (1024 + z) twice
+  f16x2 zh;  // -(64 + z) twice
   f16x2 s;   // scale twice
 };
 struct ZSbf {
@@ -74,6 +75,16 @@ __device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
   return v;
 }
 
+// Loop-invariant dequantisation constants, held in VGPRs (see and_or).
+struct DqK {
+  uint32_t lo;     // 0x000F000F: nibbles 0 and 4 of a word
+  uint32_t hi;     // 0x00F000F0: nibbles 1 and 5
+  uint32_t magic;  // 0x64006400: the fp16 pair (1024, 1024)
+};
+__device__ __forceinline__ DqK dq_consts() {
+  return DqK{opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
+}
+
 // Typed load at a 32-bit byte offset from a uniform base pointer, so the
 // compiler can use the global_load saddr form (SGPR base + VGPR offset)
 // instead of per-lane 64-bit address arithmetic.
@@ -89,29 +100,37 @@ __device__ __forceinline__ T ld_off_nt(const void* base, uint32_t byte_off) {
 template <typename DT>
 struct Dq;
 
-// fp16: (w >> 4i) & 0x000F000F | 0x6400 6400 is the fp16 pair (1024 + q_lo,
-// 1024 + q_hi) exactly; subtracting (1024 + z) is exact (integers below 2048),
-// and the one packed multiply by the scale is the single round-to-nearest-even
-// of (q - z) * s that the oracle specifies.
+// fp16, per 32-bit word (pairs i = rows (2i, 2i+1) = nibbles (i, i + 4)):
+//   nibbles 0,4:  w & 0x000F000F | 0x64006400   = the pair (1024 + q)
+//   nibbles 1,5:  w & 0x00F000F0 | 0x64006400   = the pair (1024 + 16 q)
+//   nibbles 2,6 and 3,7: the same on w >> 8.
+// (1024 + q) - (1024 + z) and fma(1024 + 16 q, 1/16, -(64 + z)) are both the
+// exact integer q - z (fp16 integers below 2048, power-of-two scaling), and
+// the one packed multiply by the scale is the single round-to-nearest-even
+// of (q - z) * s that the oracle specifies: 13 VALU operations per word.
 template <>
 struct Dq<F16> {
   using ZS = ZS16;
   __device__ __forceinline__ static ZS make(uint32_t z, uint16_t sbits) {
     ZS r;
-    uint32_t zb = 0x6400u | z;
+    const uint32_t zb = 0x6400u | z;
+    const uint32_t zh = 0xD400u | (z << 4);
     r.zb = __builtin_bit_cast(f16x2, zb | (zb << 16));
+    r.zh = __builtin_bit_cast(f16x2, zh | (zh << 16));
     r.s = __builtin_bit_cast(f16x2, (uint32_t)sbits | ((uint32_t)sbits << 16));
     return r;
   }
-  __device__ __forceinline__ static f16x8 word(uint32_t w, const ZS& zs) {
-    const uint32_t a0 = and_or(w, 0x000F000Fu, 0x64006400u);
-    const uint32_t a1 = and_or(w >> 4, 0x000F000Fu, 0x64006400u);
-    const uint32_t a2 = and_or(w >> 8, 0x000F000Fu, 0x64006400u);
-    const uint32_t a3 = and_or(w >> 12, 0x000F000Fu, 0x64006400u);
-    const f16x2 h0 = (__builtin_bit_cast(f16x2, a0) - zs.zb) * zs.s;
-    const f16x2 h1 = (__builtin_bit_cast(f16x2, a1) - zs.zb) * zs.s;
-    const f16x2 h2 = (__builtin_bit_cast(f16x2, a2) - zs.zb) * zs.s;
-    const f16x2 h3 = (__builtin_bit_cast(f16x2, a3) - zs.zb) * zs.s;
+  __device__ __forceinline__ static f16x8 word(uint32_t w, const ZS& zs, const DqK& k) {
+    const f16x2 inv16 = __builtin_bit_cast(f16x2, 0x2C002C00u);  // (1/16, 1/16)
+    const uint32_t w8 = w >> 8;
+    const f16x2 a0 = __builtin_bit_cast(f16x2, and_or(w, k.lo, k.magic));
+    const f16x2 a1 = __builtin_bit_cast(f16x2, and_or(w, k.hi, k.magic));
+    const f16x2 a2 = __builtin_bit_cast(f16x2, and_or(w8, k.lo, k.magic));
+    const f16x2 a3 = __builtin_bit_cast(f16x2, and_or(w8, k.hi, k.magic));
+    const f16x2 h0 = (a0 - zs.zb) * zs.s;
+    const f16x2 h1 = __builtin_elementwise_fma(a1, inv16, zs.zh) * zs.s;
+    const f16x2 h2 = (a2 - zs.zb) * zs.s;
+    const f16x2 h3 = __builtin_elementwise_fma(a3, inv16, zs.zh) * zs.s;
     const u32x4 r = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
                      __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3)};
     return __builtin_bit_cast(f16x8, r);
@@ -129,7 +148,7 @@ struct Dq<BF16> {
     r.s = __builtin_bit_cast(float, (uint32_t)sbits << 16);
     return r;
   }
-  __device__ __forceinline__ static bf16x8 word(uint32_t w, const ZS& zs) {
+  __device__ __forceinline__ static bf16x8 word(uint32_t w, const ZS& zs, const DqK&) {
     bf16x8 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(const typename DT::elem* __r
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane & 15, lg = lane >> 4;
   const int nt0 = blockIdx.x * 16 + wave * NTW;
+  const DqK dk = dq_consts();
   const int64_t m0 = (int64_t)blockIdx.y * BM;
 
   f32x4 acc[MTL][NTW];
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(const typename DT::elem* __r
       }
       V8 a[NTW];
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) a[j] = Dq<DT>::word(q[j][w], zs[j]);
+      for (int j = 0; j < NTW; ++j) a[j] = Dq<DT>::word(q[j][w], zs[j], dk);
 #pragma unroll
       for (int mt = 0; mt < MTL; ++mt) {
         const V8 b = __builtin_bit_cast(V8, xs[cur][(mt * 4 + w) * 64 + lane]);

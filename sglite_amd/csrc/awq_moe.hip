@@ -34,18 +34,35 @@ namespace sgl_awq {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Wave-level helpers.
+// Wave-level helpers.  Reductions use DPP row shifts and row broadcasts (an
+// inclusive scan that leaves the total in lane 63) and v_readlane, not
+// LDS-routed shuffles, whose latency dominates these small kernels.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float dpp_or(float v, float identity) {
+  // Lanes whose source is outside the row or masked off receive `identity`.
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                               __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                               BANK_MASK, false));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  const float id = MAX ? -INFINITY : 0.f;
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, dpp_or<kRowShr1, 0xf, 0xf>(v, id));
+  v = op(v, dpp_or<kRowShr2, 0xf, 0xf>(v, id));
+  v = op(v, dpp_or<kRowShr4, 0xf, 0xe>(v, id));
+  v = op(v, dpp_or<kRowShr8, 0xf, 0xc>(v, id));
+  v = op(v, dpp_or<kRowBcast15, 0xa, 0xf>(v, id));
+  v = op(v, dpp_or<kRowBcast31, 0xc, 0xf>(v, id));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
+__device__ __forceinline__ int read_lane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return lane == 0 ? 0ull : (~0ull >> (64 - lane)); }
 
 // ---------------------------------------------------------------------------
@@ -70,14 +87,14 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
   float mx = v[0];
 #pragma unroll
   for (int i = 1; i < EPL; ++i) mx = fmaxf(mx, v[i]);
-  mx = wave_max(mx);
+  mx = wave_reduce<true>(mx);
   float p[EPL], s = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     p[i] = lane + 64 * i < E ? expf(v[i] - mx) : 0.f;
     s += p[i];
   }
-  s = wave_sum(s);
+  s = wave_reduce<false>(s);
   const float inv = 1.f / s;
 #pragma unroll
   for (int i = 0; i < EPL; ++i) p[i] = lane + 64 * i < E ? p[i] * inv : -1.f;  // -1: never selected
@@ -94,24 +111,18 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
         bv = p[i];
         bi = lane + 64 * i;
       }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    // Every lane now holds the winner; its owner retires it.
+    const float top = wave_reduce<true>(bv);
+    uint64_t m = __ballot(bv == top);
+    int widx = read_lane(bi, __builtin_ctzll(m));
+    for (m &= m - 1; m; m &= m - 1) widx = min(widx, read_lane(bi, __builtin_ctzll(m)));  // exact ties only
 #pragma unroll
     for (int i = 0; i < EPL; ++i)
-      if (bi == lane + 64 * i) p[i] = -1.f;
+      if (widx == lane + 64 * i) p[i] = -1.f;
     if (lane == j) {
-      wsel = bv;
-      isel = bi;
+      wsel = top;
+      isel = widx;
     }
-    wsum += bv;
+    wsum += top;
   }
   if (lane < k) {
     const float w = renorm ? wsel / (wsum + 1e-8f) : wsel;
@@ -135,6 +146,8 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kMaxExperts = 512;
+constexpr int kIdsPerThread = 4;  // ids held in registers per pass over the input
+constexpr int kAlignChunk = kAlignThreads * kIdsPerThread;
 
 __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __restrict__ ids, int n, int E, int bs,
                                                               int32_t* __restrict__ sorted, int32_t* __restrict__ expert_ids,
@@ -143,15 +156,29 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts + 1];
   __shared__ int cursor[kMaxExperts];
-  __shared__ int wcnt[kAlignWaves][kMaxExperts];
   __shared__ int wtot[kAlignWaves];
+  // Lanes of wave w whose row goes to expert e, for the 1024 rows in flight.
+  __shared__ uint64_t wmask[kAlignWaves][kMaxExperts];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  for (int i = tid; i < kAlignWaves * kMaxExperts; i += kAlignThreads) (&wmask[0][0])[i] = 0;
+  // Rows c0 + r * 1024 + tid, r < kIdsPerThread, loaded together (one
+  // round trip per chunk instead of one per row).
+  int er[kIdsPerThread];
+  auto load_chunk = [&](int c0) {
+#pragma unroll
+    for (int r = 0; r < kIdsPerThread; ++r) {
+      const int i = c0 + r * kAlignThreads + tid;
+      er[r] = i < n ? ids[i] : -1;
+    }
+  };
   __syncthreads();
-  for (int i = tid; i < n; i += kAlignThreads) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  for (int c0 = 0; c0 < n; c0 += kAlignChunk) {
+    load_chunk(c0);
+#pragma unroll
+    for (int r = 0; r < kIdsPerThread; ++r)
+      if (er[r] >= 0 && er[r] < E) atomicAdd(&cnt[er[r]], 1);
   }
   __syncthreads();
 
@@ -183,37 +210,35 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
   }
   for (int b = total / bs + tid; b < blocks_cap; b += kAlignThreads) expert_ids[b] = -1;
 
-  // Stable scatter, 1024 rows at a time: rank within the wave by ballots,
-  // then the counts of the lower waves, then the bucket cursor.
-  for (int c0 = 0; c0 < n; c0 += kAlignThreads) {
-    for (int idx = tid; idx < kAlignWaves * E; idx += kAlignThreads) wcnt[idx / E][idx % E] = 0;
-    __syncthreads();
-    const int i = c0 + tid;
-    const int e = i < n ? ids[i] : -1;
-    const bool valid = e >= 0 && e < E;
-    int rank = 0;
-    uint64_t todo = __ballot(valid);
-    while (todo) {
-      const int leader = __builtin_ctzll(todo);
-      const int le = __shfl(e, leader);
-      const uint64_t mask = __ballot(valid && e == le);
-      if (valid && e == le) rank = __popcll(mask & lanes_below(lane));
-      if (lane == leader) wcnt[wave][le] = __popcll(mask);
-      todo &= ~mask;
+  // Stable scatter, 1024 rows at a time: a row's position is its bucket's
+  // cursor, plus the rows of the same expert in lower waves, plus those in
+  // lower lanes of its own wave (all popcounts of the lane masks).
+  for (int c0 = 0; c0 < n; c0 += kAlignChunk) {
+    if (c0 > 0 || n > kAlignChunk) load_chunk(c0);  // a single chunk is still in registers
+#pragma unroll
+    for (int r = 0; r < kIdsPerThread; ++r) {
+      if (c0 + r * kAlignThreads >= n) break;  // uniform
+      const int i = c0 + r * kAlignThreads + tid;
+      const int e = er[r];
+      const bool valid = e >= 0 && e < E;
+      if (valid) atomicOr((unsigned long long*)&wmask[wave][e], 1ull << lane);
+      __syncthreads();
+      if (valid) {
+        const uint64_t m = wmask[wave][e];
+        int pos = cursor[e] + __popcll(m & lanes_below(lane));
+        for (int w = 0; w < wave; ++w) pos += __popcll(wmask[w][e]);
+        sorted[pos] = i;
+      }
+      __syncthreads();
+      for (int ee = tid; ee < E; ee += kAlignThreads) {
+        int s = 0;
+        for (int w = 0; w < kAlignWaves; ++w) s += __popcll(wmask[w][ee]);
+        cursor[ee] += s;
+      }
+      __syncthreads();
+      if (valid) wmask[wave][e] = 0;  // every lane of the group writes the same zero
+      __syncthreads();
     }
-    __syncthreads();
-    if (valid) {
-      int pos = cursor[e] + rank;
-      for (int w = 0; w < wave; ++w) pos += wcnt[w][e];
-      sorted[pos] = i;
-    }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += kAlignThreads) {
-      int s = 0;
-      for (int w = 0; w < kAlignWaves; ++w) s += wcnt[w][ee];
-      cursor[ee] += s;
-    }
-    __syncthreads();
   }
 }
 
@@ -248,77 +273,105 @@ struct MoeArgs {
   int mul_rw;
 };
 
-// Routed rows per pass: kMaxMt m-tiles of 16.  Two keep the kernel within
-// the register budget of three workgroups per CU (the weight stream needs that
-// many loads in flight); an expert with more rows takes more passes, spread
-// over grid.y so that they run side by side and share the weights through L2.
-constexpr int kMaxMt = 2;
+// Workgroup shape: 8 waves, each owning two 16-column tiles (256 columns per
+// workgroup, or 128 gate + 128 up columns with a gate/up activation), so the
+// gathered activation tile in LDS feeds 16 tiles while each wave's prefetch
+// state stays small enough for two workgroups per CU with three k-tiles of
+// loads in flight per wave.
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kTilesPerWave = 2;
+// Routed rows per pass: up to kMaxMt m-tiles of 16.  An expert with more rows
+// takes more passes, spread over grid.y so that they run side by side and
+// share the expert's weights through L2.
+constexpr int kMaxMt = 4;
 constexpr int kXsBuf = kMaxMt * 4 * 64;  // one LDS buffer: [m-tile][k-block][lane]
+constexpr int kXsBufs = 2;
 
 // One pass over K for MC m-tiles (16 routed rows each) starting at sorted row
-// rb.  The wave's four column tiles are ntc[0..3] of expert-local tile index.
+// rb.  The wave's column tiles are ntc[0..1] (expert-local tile indices).
 template <int MC, int GPT, int EPI, typename DT>
 __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ xs, const u32x4* __restrict__ we,
                                          const uint16_t* __restrict__ se, const uint64_t* __restrict__ ze,
-                                         const int (&ntc)[4], const int (&ncol)[4], int rb, int wave, int lane) {
+                                         const int (&ntc)[kTilesPerWave], const int (&ncol)[kTilesPerWave], int rb,
+                                         int wave, int lane) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
   using V4 = typename DT::vec4;
   using ZS = typename Dq<DT>::ZS;
-  constexpr int BPG = 4 / GPT;  // 32-row k-blocks per group
+  constexpr int TW = kTilesPerWave;
+  constexpr int BPG = 4 / GPT;                           // 32-row k-blocks per group
+  constexpr int NFRAG = MC * 4;                          // activation fragments per k-tile
+  constexpr int FPT = (NFRAG + kWaves - 1) / kWaves;     // fragments loaded per thread
   const int c = lane & 15, lg = lane >> 4;
   const void* x = a.x;
+  const DqK dk = dq_consts();
 
-  // Routed row of lane column c in m-tile i (loader and epilogue share it).
+  // Routed row of lane column c in each m-tile (the loader and the epilogue
+  // share it); padding rows read activation row 0 and are never stored (MFMA
+  // output column m depends on activation row m only).
   int sid[MC];
-  uint32_t xoff[MC];  // byte offset of the row (the host keeps `a` below 4 GiB)
-  bool xval[MC];
+  bool sval[MC];
 #pragma unroll
   for (int i = 0; i < MC; ++i) {
     sid[i] = a.sorted[rb + i * 16 + c];
-    xval[i] = sid[i] >= 0 && sid[i] < a.num_routed;
-    xoff[i] = (uint32_t)(xval[i] ? sid[i] / a.a_div : 0) * (uint32_t)a.K * 2u;
+    sval[i] = sid[i] >= 0 && sid[i] < a.num_routed;
+  }
+  // Loader: thread (wave, lane) fetches fragments f = wave + kWaves * i
+  // (m-tile f / 4, k-block f % 4) of each k-tile.
+  uint32_t xrow[FPT];  // byte offset of the fragment's row (the host keeps `a` below 4 GiB)
+#pragma unroll
+  for (int i = 0; i < FPT; ++i) {
+    const int mt = min(wave + kWaves * i, NFRAG - 1) >> 2;
+    int r = 0;
+#pragma unroll
+    for (int m = 0; m < MC; ++m)
+      if (m == mt) r = sval[m] ? sid[m] / a.a_div : 0;
+    xrow[i] = (uint32_t)r * (uint32_t)a.K * 2u;
   }
 
-  f32x4 acc[MC][4];
+  f32x4 acc[MC][TW];
 #pragma unroll
   for (int mt = 0; mt < MC; ++mt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Per-tile byte offsets inside the expert.
-  uint32_t woff[4], goff[4];
+  uint32_t woff[TW], goff[TW];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < TW; ++j) {
     woff[j] = ((uint32_t)ntc[j] * (uint32_t)a.KT * 64u + lane) * 16u;
     goff[j] = (uint32_t)ntc[j] * (uint32_t)a.NG;
   }
 
-  // Everything one k-tile needs from global memory.  Two stages alternate
-  // (the loop is unrolled by two) so that no register copy waits for the
-  // prefetched loads before their use.
+  // Everything one k-tile needs from global memory.  Three stages rotate
+  // (the loop is unrolled by three, so no register copy waits for a load):
+  // weights are loaded two k-tiles ahead of their use, activations two tiles
+  // ahead of their LDS store.
   struct Stage {
-    u32x4 q[4];           // weight words of the four column tiles
-    uint32_t z[4][GPT];   // zero-point word holding the lane's nibble
-    uint32_t s[4][GPT];   // scale bits
-    u32x4 xr[MC];         // activation fragments bound for LDS
+    u32x4 q[TW];           // weight words of the wave's column tiles
+    uint32_t z[TW][GPT];   // zero-point word holding the lane's nibble
+    uint16_t s[TW][GPT];   // scale bits (kept 16-bit: a widening would wait for the load at once)
+    u32x4 xr[FPT];         // activation fragments bound for LDS
   };
-
-  // Rows of padding read activation row 0 and are never stored (MFMA output
-  // column m depends on activation row m only).  k-blocks past K (K % 128 != 0)
-  // are zeroed when they are written to LDS, so the loads themselves carry no
-  // select that would make the wave wait for them right after issue.
   auto load = [&](int kt, Stage& st) {
-    const uint32_t koff = (uint32_t)min(kt * 128 + wave * 32, a.K - 32) * 2u + (uint32_t)lg * 16u;
+    // k-blocks past K (K % 128 != 0) read the row's last k-block and are
+    // zeroed when stored, so the loads carry no select that would wait for them.
+    // Waves without a fragment of their own reload the last one (branches
+    // around loads make the compiler wait for every load at the join).
 #pragma unroll
-    for (int i = 0; i < MC; ++i) st.xr[i] = ld_off<u32x4>(x, xoff[i] + koff);
+    for (int i = 0; i < FPT; ++i) {
+      const int f = min(wave + kWaves * i, NFRAG - 1);
+      const uint32_t k0 = (uint32_t)min(kt * 128 + (f & 3) * 32, a.K - 32);
+      st.xr[i] = ld_off<u32x4>(x, xrow[i] + (k0 + (uint32_t)lg * 8u) * 2u);
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st.q[j] = ld_off_nt<u32x4>(we, woff[j] + (uint32_t)kt * 1024u);
+    for (int j = 0; j < TW; ++j) st.q[j] = ld_off_nt<u32x4>(we, woff[j] + (uint32_t)kt * 1024u);
 #pragma unroll
     for (int gg = 0; gg < GPT; ++gg) {
       const uint32_t g = (uint32_t)min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TW; ++j) {
         const uint32_t gi = goff[j] + g;
         st.z[j][gg] = ld_off<uint32_t>(ze, gi * 8u + (uint32_t)(c >> 3) * 4u);
         st.s[j][gg] = ld_off<uint16_t>(se, (gi * 16u + c) * 2u);
@@ -326,55 +379,61 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
     }
   };
   auto store_x = [&](const Stage& st, int kt) {
-    const bool kval = kt * 128 + wave * 32 < a.K;
-    const int buf = kt & 1;
+    u32x4* buf = xs + (kt & 1) * kXsBuf;
 #pragma unroll
-    for (int i = 0; i < MC; ++i)
-      xs[buf * kXsBuf + (i * 4 + wave) * 64 + lane] = kval ? st.xr[i] : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < FPT; ++i) {
+      const int f = wave + kWaves * i;
+      if (f < NFRAG) {
+        const bool kval = kt * 128 + (f & 3) * 32 < a.K;
+        buf[f * 64 + lane] = kval ? st.xr[i] : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
   };
   auto compute = [&](const Stage& st, int kt) {
-    const int buf = kt & 1;
+    const u32x4* buf = xs + (kt & 1) * kXsBuf;
 #pragma unroll
     for (int gg = 0; gg < GPT; ++gg) {
-      ZS zs[4];
+      ZS zs[TW];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) zs[j] = Dq<DT>::make((st.z[j][gg] >> (4 * (c & 7))) & 0xFu, (uint16_t)st.s[j][gg]);
+      for (int j = 0; j < TW; ++j) zs[j] = Dq<DT>::make((st.z[j][gg] >> (4 * (c & 7))) & 0xFu, st.s[j][gg]);
 #pragma unroll
       for (int b = 0; b < BPG; ++b) {
         const int w = gg * BPG + b;  // k-blocks past K meet zeroed activations
-        V8 av[4];
+        V8 av[TW];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = Dq<DT>::word(st.q[j][w], zs[j]);
+        for (int j = 0; j < TW; ++j) av[j] = Dq<DT>::word(st.q[j][w], zs[j], dk);
 #pragma unroll
         for (int mt = 0; mt < MC; ++mt) {
-          const V8 bx = __builtin_bit_cast(V8, xs[buf * kXsBuf + (mt * 4 + w) * 64 + lane]);
+          const V8 bx = __builtin_bit_cast(V8, buf[(mt * 4 + w) * 64 + lane]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
+          for (int j = 0; j < TW; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
         }
       }
     }
   };
-  // One k-tile: prefetch the next (the last tile reloads itself, so the loads
-  // are unconditional), compute this one, publish the next tile's activations.
-  auto step = [&](int kt, const Stage& cur, Stage& nxt) {
-    const int nk = min(kt + 1, a.KT - 1);
-    load(nk, nxt);
+  // One k-tile: prefetch tile kt + 2 (past the end the last tile reloads
+  // itself, so the loads are unconditional), compute tile kt, publish tile
+  // kt + 1's activations to the other LDS buffer.
+  auto step = [&](int kt, const Stage& cur, const Stage& nxt1, Stage& nxt2) {
+    load(min(kt + 2, a.KT - 1), nxt2);
     // Keep the prefetch ahead of this tile's math (the scheduler would
     // otherwise start the math first, waiting for this tile's loads while the
-    // next tile's are not yet issued).
+    // later tiles' are not yet issued).
     __builtin_amdgcn_sched_barrier(0);
     compute(cur, kt);
-    store_x(nxt, kt + 1);
+    store_x(nxt1, kt + 1);
     __syncthreads();
   };
 
-  Stage sa, sb;
-  load(0, sa);
-  store_x(sa, 0);
+  Stage s0, s1, s2;
+  load(0, s0);
+  load(min(1, a.KT - 1), s1);
+  store_x(s0, 0);
   __syncthreads();
-  for (int kt = 0; kt < a.KT; kt += 2) {
-    step(kt, sa, sb);
-    if (kt + 1 < a.KT) step(kt + 1, sb, sa);
+  for (int kt = 0; kt < a.KT; kt += 3) {
+    step(kt, s0, s1, s2);
+    if (kt + 1 < a.KT) step(kt + 1, s1, s2, s0);
+    if (kt + 2 < a.KT) step(kt + 2, s2, s0, s1);
   }
 
   // Epilogue: lane (c, lg) of fragment (mt, j) holds row c of m-tile mt and
@@ -382,11 +441,11 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   E* out = (E*)a.out;
 #pragma unroll
   for (int mt = 0; mt < MC; ++mt) {
-    if (!xval[mt]) continue;
+    if (!sval[mt]) continue;
     const float rw = a.mul_rw ? a.topk_w[sid[mt]] : 1.f;
     if constexpr (EPI == kEpiPlain) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < TW; ++j) {
         if (ncol[j] < 0 || ncol[j] + 4 * lg >= a.N) continue;  // N % 16 == 8: half of the last tile
         V4 r;
 #pragma unroll
@@ -394,28 +453,24 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
         *(V4*)(out + (int64_t)sid[mt] * a.N + ncol[j] + 4 * lg) = r;
       }
     } else {
-      // Tiles 0, 1 are gate tiles and 2, 3 the matching up tiles; the first
+      // Tile 0 is a gate tile and tile 1 the matching up tile; the first
       // GEMM's output is rounded before the activation (fused.py:175-177).
-      const int I = a.N >> 1;
+      if (ncol[0] < 0) continue;
+      V4 r;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (ncol[j] < 0) continue;
-        V4 r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float g = (float)(E)(acc[mt][j][i] * rw);
-          const float u = (float)(E)(acc[mt][j + 2][i] * rw);
-          r[i] = (E)(gate_act<EPI>(g) * u);
-        }
-        *(V4*)(out + (int64_t)sid[mt] * I + ncol[j] + 4 * lg) = r;
+      for (int i = 0; i < 4; ++i) {
+        const float g = (float)(E)(acc[mt][0][i] * rw);
+        const float u = (float)(E)(acc[mt][1][i] * rw);
+        r[i] = (E)(gate_act<EPI>(g) * u);
       }
+      *(V4*)(out + (int64_t)sid[mt] * (a.N >> 1) + ncol[0] + 4 * lg) = r;
     }
   }
 }
 
 template <int GPT, int EPI, typename DT>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(MoeArgs a) {
-  __shared__ u32x4 xs[2 * kXsBuf];
+__global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
+  __shared__ u32x4 xs[kXsBufs * kXsBuf];
   // XCD-aware placement: workgroup b runs on XCD b % 8; logical index L
   // walks the column slices of one expert on one XCD.
   const int per = gridDim.x >> 3;
@@ -428,36 +483,34 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(MoeArgs a) {
   if ((int)blockIdx.y * kMaxMt >= nblk) return;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int ntc[4], ncol[4];
+  int ntc[kTilesPerWave], ncol[kTilesPerWave];
   if constexpr (EPI == kEpiPlain) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nt = slice * 16 + wave * 4 + j;
+    for (int j = 0; j < kTilesPerWave; ++j) {
+      const int nt = (slice * kWaves + wave) * kTilesPerWave + j;
       ntc[j] = min(nt, a.NT - 1);
-      ncol[j] = nt < a.NT && nt * 16 < a.N ? nt * 16 : -1;
+      ncol[j] = nt < a.NT ? nt * 16 : -1;
     }
   } else {
     const int NTg = a.NT >> 1;  // gate tiles; up tile of gate tile t is t + NTg
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int gt = slice * 8 + wave * 2 + j;
-      ntc[j] = min(gt, NTg - 1);
-      ntc[j + 2] = ntc[j] + NTg;
-      ncol[j] = gt < NTg ? gt * 16 : -1;
-      ncol[j + 2] = -1;
-    }
+    const int gt = slice * kWaves + wave;
+    ntc[0] = min(gt, NTg - 1);
+    ntc[1] = ntc[0] + NTg;
+    ncol[0] = gt < NTg ? gt * 16 : -1;
+    ncol[1] = -1;
   }
   const u32x4* we = a.wt + e * a.w_stride;
   const uint16_t* se = a.s_r + e * a.s_stride;
   const uint64_t* ze = a.z_r + e * a.z_stride;
 
-  static_assert(kMaxMt == 2, "pass dispatch below covers one and two m-tiles");
   for (int p = blockIdx.y; p * kMaxMt < nblk; p += gridDim.y) {
     const int rb = r0 + p * kMaxMt * 16;
-    if (nblk - p * kMaxMt >= 2)
-      moe_pass<2, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane);
-    else
-      moe_pass<1, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane);
+    switch (min(nblk - p * kMaxMt, kMaxMt)) {
+      case 1: moe_pass<1, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 2: moe_pass<2, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 3: moe_pass<3, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      default: moe_pass<4, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+    }
     __syncthreads();  // the next pass refills both LDS buffers
   }
 }
@@ -493,7 +546,7 @@ hipError_t launch_moe_gemm_dt(const MoeArgs& a, int gpt, int epi, int passes, hi
   dim3 grid((unsigned)gx, (unsigned)passes);
 #define SGL_MOE(GPT_, EPI_)                                                                 \
   if (gpt == GPT_ && epi == EPI_) {                                                         \
-    hipLaunchKernelGGL((moe_gemm_kernel<GPT_, EPI_, DT>), grid, dim3(256), 0, s, a);        \
+    hipLaunchKernelGGL((moe_gemm_kernel<GPT_, EPI_, DT>), grid, dim3(kThreads), 0, s, a);   \
     return hipGetLastError();                                                               \
   }
 #define SGL_MOE_E(GPT_) SGL_MOE(GPT_, kEpiPlain) SGL_MOE(GPT_, kEpiSilu) SGL_MOE(GPT_, kEpiGelu)
@@ -555,7 +608,8 @@ hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s) {
   a.w_stride = st.w / 16;
   a.s_stride = st.s / 2;
   a.z_stride = st.z / 8;
-  a.S = p.epi == kEpiPlain ? (int)((p.g.NT + 15) / 16) : (int)((p.g.NT / 2 + 7) / 8);
+  a.S = p.epi == kEpiPlain ? (int)((p.g.NT + kWaves * kTilesPerWave - 1) / (kWaves * kTilesPerWave))
+                            : (int)((p.g.NT / 2 + kWaves - 1) / kWaves);
   a.total = a.S * (int)p.E;
   a.mul_rw = p.mul_rw;
   const int gpt = (p.g.NG > 1 && p.g.G < 128) ? (int)(128 / p.g.G) : 1;

@@ -144,7 +144,7 @@ __global__ void dequant_repacked_kernel(const u32x4* __restrict__ wt, const uint
     if (kb >= K) continue;
     const int64_t g = kb >> gshift;
     const auto zs = Dq<DT>::make(zero_nibble(z_r[nt * NG + g], c), s_r[(nt * NG + g) * 16 + c]);
-    const auto v = Dq<DT>::word(q[w], zs);
+    const auto v = Dq<DT>::word(q[w], zs, dq_consts());
     if (n < N) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) out[(kb + lg * 8 + e) * N + n] = v[e];
