@@ -194,8 +194,56 @@ hipError_t launch_tiled_dt(const GemmPlan& p, const void* x, const void* w, cons
 
 }  // namespace
 
+// GEMV plan (small M): every wave issues the loads of all its k-tiles at
+// once.  From a sweep of the variants and splits over the Qwen3-4B and
+// Llama-3-8B decode shapes on MI355X: one column tile per workgroup; 8 waves
+// of at most 4 k-tiles (4 waves of at most 8 for layers of >= 1024 column
+// tiles, where the grid alone fills the chip); the smallest split-K that
+// keeps each wave within its k-tile budget.  Larger batches (>= 8 rows)
+// stage too much activation per workgroup and use the wider decode kernel.
+constexpr int kGemvMaxM = 4;
+
+bool plan_gemv(const Geom& g, GemmPlan& p) {
+  int ntw = 1, wk = g.NT >= 1024 ? 4 : 8, kpw = g.NT >= 1024 ? 8 : 4;
+  const int env = env_int("SGL_AWQ_GEMV_VARIANT", 0);
+  if (gemv_variant_ok(env)) {
+    ntw = env / 1000;
+    wk = (env / 10) % 100;
+    kpw = env % 10;
+  }
+  const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
+  if (gpt > 1) kpw = std::min(kpw, 4);  // zero words and scales per k-tile grow with gpt
+  const int64_t gx = (g.NT + ntw - 1) / ntw;
+  int64_t ks = std::max<int64_t>(1, (g.KT + (int64_t)wk * kpw - 1) / ((int64_t)wk * kpw));
+  const int env_ks = env_int("SGL_AWQ_GEMV_KS", 0);
+  if (env_ks > 0) ks = env_ks;
+  for (;;) {
+    ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
+    const int64_t ktc = (g.KT + ks - 1) / ks;
+    const int64_t chunks = g.M * ktc * 16;
+    const int64_t xpt = (chunks + 64 * wk - 1) / (64 * wk);
+    if ((ktc + wk - 1) / wk > kpw || xpt > 4) {
+      if (ks >= g.KT) return false;
+      ks *= 2;
+      continue;
+    }
+    if (!gemv_variant_ok(ntw * 1000 + wk * 10 + kpw)) return false;
+    p.kind = 2;
+    p.variant = ntw * 1000 + wk * 10 + kpw;
+    p.ktc = (int)ktc;
+    p.ks = (int)((g.KT + ktc - 1) / ktc);
+    p.xpt = xpt <= 1 ? 1 : (xpt <= 2 ? 2 : 4);
+    p.grid_x = gx;
+    p.grid_y = p.ks;
+    p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
+    p.lds_bytes = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * ntw * 1024);
+    return true;
+  }
+}
+
 GemmPlan plan_gemm(const Geom& g) {
   GemmPlan p{};
+  if (g.M <= env_int("SGL_AWQ_GEMV_MAX_M", kGemvMaxM) && g.M <= 16 && plan_gemv(g, p)) return p;
   if (g.M <= 32) {
     p.kind = 0;
     // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all
@@ -260,6 +308,7 @@ hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const vo
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s) {
   if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
+  if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
   return dtype == 0 ? launch_tiled_dt<F16>(p, x, w, sr, zr, bias, out, g, s)
                     : launch_tiled_dt<BF16>(p, x, w, sr, zr, bias, out, g, s);
 }

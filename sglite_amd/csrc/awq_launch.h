@@ -25,18 +25,24 @@ hipError_t launch_dequant_repacked(const void* w, const void* sr, const void* zr
 
 // GEMM plan: which kernel and how K is split.
 struct GemmPlan {
-  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM
+  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM, 2 = GEMV (M <= 16)
   int variant;   // kernel template selector
-  int ks;        // k-splits across workgroups (skinny)
-  int ktc;       // k-tiles per workgroup (skinny)
+  int ks;        // k-splits across workgroups (skinny, GEMV)
+  int ktc;       // k-tiles per workgroup (skinny, GEMV)
+  int xpt;       // activation chunks per thread (GEMV)
   int64_t grid_x, grid_y;
   int64_t ws_bytes;
+  int64_t lds_bytes;  // dynamic LDS (GEMV)
 };
 
 GemmPlan plan_gemm(const Geom& g);
 hipError_t launch_skinny(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                          const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                          hipStream_t s);
+bool gemv_variant_ok(int v);
+hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       hipStream_t s);
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);

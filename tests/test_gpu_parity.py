@@ -300,6 +300,7 @@ def test_every_decode_variant(variant, G, monkeypatch):
     t, d = _linear(K, N, G, seed=variant * 7 + G)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
+    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "0")  # M = 1 too through this kernel
     for ks in (1, 3):
         monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
         monkeypatch.setenv("SGL_AWQ_SKINNY_KS", str(ks))
@@ -321,8 +322,49 @@ def test_decode_bf16_variants(M, monkeypatch):
     cnt = ops.make_counters(N, DEV)
     x = oracle.make_activation(M, K, seed=78, dtype=torch.bfloat16)
     ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "0")
     for variant in (10116, 20202, 10401):
         monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
         y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
         ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
         assert ok, (variant, err, mx)
+
+
+@pytest.mark.parametrize("variant", [1044, 1048, 1084, 2044, 2048, 2028])
+@pytest.mark.parametrize("G", [128, 64, 32, -1])
+def test_every_gemv_variant(variant, G, monkeypatch):
+    """Each small-batch GEMV instantiation, with and without cross-workgroup
+    split-K, for every batch size it accepts (1..16 rows), on a K with a
+    partial last 128-row tile where G allows and N % 16 == 8."""
+    ops = _ops()
+    K = {32: 2336, 64: 2368, 128: 2432, -1: 2432}[G]
+    N = 200
+    t, d = _linear(K, N, G, seed=variant * 11 + (G if G > 0 else 7))
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "16")
+    monkeypatch.setenv("SGL_AWQ_GEMV_VARIANT", str(variant))
+    for ks in (1, 3):
+        monkeypatch.setenv("SGL_AWQ_GEMV_KS", str(ks))
+        for M in (1, 3, 4, 16):
+            x = oracle.make_activation(M, K, seed=M + ks)
+            y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
+            ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+            ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+            assert ok, (variant, G, ks, M, err, mx)
+        assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_bf16_and_bias(M):
+    ops = _ops()
+    K, N, G = 4096, 136, 128
+    t, d = _linear(K, N, G, seed=91 + M, dtype=torch.bfloat16)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    x = oracle.make_activation(M, K, seed=92, dtype=torch.bfloat16)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(93)).to(torch.bfloat16)
+    ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], bias, G)
+    y = ops.gemm(x.to(DEV), r, K, N, G, bias=bias.to(DEV), counters=cnt)
+    ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+    assert ok, (err, mx)
