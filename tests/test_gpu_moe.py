@@ -322,3 +322,31 @@ def test_fused_experts_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(buf, eager), i
         _ = (x.float() @ x.float().T).sum().item()  # unrelated eager work between replays
+
+
+def test_checkpoint_stream_to_fused_experts():
+    """Per-expert AWQ checkpoint tensors (gate/up/down of each expert) ->
+    ingest (gate/up merged on packed columns, experts stacked) -> repack ->
+    fused experts, against the oracle on the logical weights."""
+    from sglite_amd import checkpoint
+    from sglite_amd.moe import fused_experts_impl, process_awq_moe_weights
+    T, E, k, H, I, G = 20, 6, 2, 256, 128, 64
+    W1, W2 = _moe_weights(E, H, I, G, seed=300)
+    stream = []
+    for e in range(E):
+        for suffix in ("qweight", "qzeros", "scales"):
+            gu = W1[suffix][e]
+            half = gu.shape[1] // 2
+            stream.append((f"model.layers.3.mlp.experts.{e}.gate_proj.{suffix}", gu[:, :half].contiguous()))
+            stream.append((f"model.layers.3.mlp.experts.{e}.up_proj.{suffix}", gu[:, half:].contiguous()))
+            stream.append((f"model.layers.3.mlp.experts.{e}.down_proj.{suffix}", W2[suffix][e]))
+    out = dict(checkpoint.ingest(stream, num_experts=E, dtype=torch.float16))
+    pre = "model.layers.3.mlp.experts."
+    w1 = process_awq_moe_weights(*(out[pre + "gate_up_proj." + s].to(DEV) for s in ("qweight", "qzeros", "scales")))
+    w2 = process_awq_moe_weights(*(out[pre + "down_proj." + s].to(DEV) for s in ("qweight", "qzeros", "scales")))
+    _, tw, ids = _routing(T, E, k, seed=301)
+    x = oracle.make_activation(T, H, seed=302)
+    ref = oracle.fused_moe_awq(x, W1, W2, tw, ids, G)
+    got = fused_experts_impl(x.to(DEV), w1, w2, tw.to(DEV), ids.to(DEV), "silu")
+    ok, err, mx = oracle.tolerance_ok(got.cpu(), ref, TOL)
+    assert ok, (err, mx)
