@@ -194,56 +194,63 @@ hipError_t launch_tiled_dt(const GemmPlan& p, const void* x, const void* w, cons
 
 }  // namespace
 
-// GEMV plan (small M): every wave issues the loads of all its k-tiles at
-// once.  From a sweep of the variants and splits over the Qwen3-4B and
-// Llama-3-8B decode shapes on MI355X: one column tile per workgroup; 8 waves
-// of at most 4 k-tiles (4 waves of at most 8 for layers of >= 1024 column
-// tiles, where the grid alone fills the chip); the smallest split-K that
-// keeps each wave within its k-tile budget.  Larger batches (>= 8 rows)
-// stage too much activation per workgroup and use the wider decode kernel.
-constexpr int kGemvMaxM = 4;
+// GEMV plan (small M, one quantisation group per 128-row tile): every wave
+// issues the loads of all its k-tiles at once.  Variant code
+// ntw * 10000 + wn * 1000 + wk * 10 + kpw.  The rules come from a sweep of the
+// variants and splits over the Qwen3-4B and Llama-3-8B decode shapes on
+// MI355X; the split-K is the smallest that keeps each wave within its k-tile
+// budget and the workgroup's activation slice within 8 loads per thread and
+// 64 KiB of LDS.
+// Where the GEMV kernel wins (same sweep): M <= 4, and M <= 8 on K <= 3072;
+// at larger M the per-workgroup activation slice costs more than the wider
+// decode kernel's per-wave fragments.
+bool gemv_preferred(const Geom& g) {
+  const int forced = env_int("SGL_AWQ_GEMV_MAX_M", -1);
+  if (forced >= 0) return g.M <= forced;
+  return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
+}
+
+// 8 waves of at most 4 k-tiles, one column tile per workgroup.
+int gemv_default_variant(const Geom&) { return 11084; }
 
 bool plan_gemv(const Geom& g, GemmPlan& p) {
-  int ntw = 1, wk = g.NT >= 1024 ? 4 : 8, kpw = g.NT >= 1024 ? 8 : 4;
+  if (g.NG > 1 && g.G < 128) return false;
+  int v = gemv_default_variant(g);
   const int env = env_int("SGL_AWQ_GEMV_VARIANT", 0);
-  if (gemv_variant_ok(env)) {
-    ntw = env / 1000;
-    wk = (env / 10) % 100;
-    kpw = env % 10;
-  }
-  const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
-  if (gpt > 1) kpw = std::min(kpw, 4);  // zero words and scales per k-tile grow with gpt
-  const int64_t gx = (g.NT + ntw - 1) / ntw;
+  if (gemv_variant_ok(env)) v = env;
+  if (!gemv_variant_ok(v)) return false;
+  const int ntw = v / 10000, wn = (v / 1000) % 10, wk = (v / 10) % 100, kpw = v % 10;
+  const int64_t mt = (g.M + 15) / 16, threads = 64 * wn * wk;
+  const int64_t gx = (g.NT + (int64_t)wn * ntw - 1) / ((int64_t)wn * ntw);
   int64_t ks = std::max<int64_t>(1, (g.KT + (int64_t)wk * kpw - 1) / ((int64_t)wk * kpw));
   const int env_ks = env_int("SGL_AWQ_GEMV_KS", 0);
   if (env_ks > 0) ks = env_ks;
   for (;;) {
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
     const int64_t ktc = (g.KT + ks - 1) / ks;
-    const int64_t chunks = g.M * ktc * 16;
-    const int64_t xpt = (chunks + 64 * wk - 1) / (64 * wk);
-    if ((ktc + wk - 1) / wk > kpw || xpt > 4) {
+    const int64_t xpt = (g.M * ktc * 16 + threads - 1) / threads;
+    const int64_t lds = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * wn * mt * ntw * 1024);
+    if ((ktc + wk - 1) / wk > kpw || xpt > 8 || lds > 61440) {
       if (ks >= g.KT) return false;
       ks *= 2;
       continue;
     }
-    if (!gemv_variant_ok(ntw * 1000 + wk * 10 + kpw)) return false;
     p.kind = 2;
-    p.variant = ntw * 1000 + wk * 10 + kpw;
+    p.variant = v;
     p.ktc = (int)ktc;
     p.ks = (int)((g.KT + ktc - 1) / ktc);
-    p.xpt = xpt <= 1 ? 1 : (xpt <= 2 ? 2 : 4);
+    p.xpt = xpt <= 1 ? 1 : (xpt <= 2 ? 2 : (xpt <= 4 ? 4 : 8));
     p.grid_x = gx;
     p.grid_y = p.ks;
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
-    p.lds_bytes = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * ntw * 1024);
+    p.lds_bytes = lds;
     return true;
   }
 }
 
 GemmPlan plan_gemm(const Geom& g) {
   GemmPlan p{};
-  if (g.M <= env_int("SGL_AWQ_GEMV_MAX_M", kGemvMaxM) && g.M <= 16 && plan_gemv(g, p)) return p;
+  if (g.M <= 32 && gemv_preferred(g) && plan_gemv(g, p)) return p;
   if (g.M <= 32) {
     p.kind = 0;
     // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all

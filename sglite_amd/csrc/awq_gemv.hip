@@ -1,17 +1,18 @@
-// Decode GEMV-regime W4A16 kernel (M <= 16) for gfx950.
+// Decode-regime W4A16 kernel for small batches (M <= 32) for gfx950.
 //
-// Each workgroup owns NTW column tiles of 16 columns and a k-range of its
-// split-K slice; its WK waves take the slice's k-tiles round robin.  A launch
+// Each workgroup owns WN x NTW column tiles of 16 columns and a k-range of its
+// split-K slice: wave (wn, wk) takes column tiles wn*NTW .. wn*NTW + NTW - 1
+// and the slice's k-tiles wk, wk + WK, ...; MT = 1 or 2 m-tiles of 16 rows.  A launch
 // of a decode-size layer (a few MB of int4 weights) is short enough that its
 // time is set by how soon the weight loads are in flight, so a wave issues
 // the loads of every k-tile it owns (weights, zero words, scales) before it
 // computes anything, and waits for them one k-tile at a time.
 //
 // The activation slice of the workgroup (M rows x its k-range) is staged once
-// through LDS: XPT 16-byte loads per thread, issued ahead of the weight loads
-// so that their (L2) latency hides under the weights' HBM latency.  MFMA B
-// fragments are then ds_read_b128 of that slice (rows >= M read row M - 1;
-// their outputs are never stored).
+// through LDS, shared by all its waves: XPT 16-byte loads per thread, issued
+// ahead of the weight loads so that their (L2) latency hides under the
+// weights' HBM latency.  MFMA B fragments are then ds_read_b128 of that slice
+// (rows >= M read row M - 1; their outputs are never stored).
 //
 // Per k-block the weights are dequantised exactly (Dq<DT>::word, the same
 // rounding as the oracle) into the MFMA A operand and accumulated in fp32;
@@ -22,7 +23,8 @@
 //
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
-// and gptq_marlin_gemm (marlin_utils.py:388-410) for batches of up to 16 rows.
+// and gptq_marlin_gemm (marlin_utils.py:388-410) for batches of up to 32 rows
+// whose quantisation groups span whole 128-row tiles (G = 128 or G = K).
 #include <algorithm>
 
 #include "awq_device.h"
@@ -37,28 +39,29 @@ __device__ __forceinline__ float xchg_agent(float* p, float v) {
   return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NTW, int WK, int KPW, int XPT, int GPT, typename DT>
-__global__ __launch_bounds__(64 * WK) void gemv_kernel(
+template <int NTW, int WN, int WK, int KPW, int MT, int XPT, typename DT>
+__global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
     const uint64_t* __restrict__ z_r, const typename DT::elem* __restrict__ bias, typename DT::elem* __restrict__ out,
     float* __restrict__ part, int32_t* __restrict__ counters, int M, int N, int K, int NT, int KT, int NG, int gshift,
     int ktc, int KS) {
   using V8 = typename DT::vec8;
   using ZS = typename Dq<DT>::ZS;
-  constexpr int NTHREADS = 64 * WK;
-  constexpr int BPG = 4 / GPT;  // 32-row k-blocks per group
+  constexpr int NTHREADS = 64 * WN * WK;
+  constexpr int NTG = WN * NTW;  // column tiles of the workgroup
   // LDS: the activation slice (M x ktc*128 halves, row stride ktc*128 + 8), then
-  // (after a barrier) the WK x NTW x 256 partial sums of the reduction.
+  // (after a barrier) the WK partial sums of every output quad.
   extern __shared__ u32x4 smem[];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wn = wave % WN, wk = wave / WN;
   const int c = lane & 15, lg = lane >> 4;
-  const int nt0 = blockIdx.x * NTW;
+  const int nt0 = blockIdx.x * NTG + wn * NTW;
   const int kt_begin = blockIdx.y * ktc;
   const int kt_end = min(kt_begin + ktc, KT);
-  const int nkt = kt_end - kt_begin;                        // k-tiles of this workgroup
-  const int kpw = wave < nkt ? (nkt - 1 - wave) / WK + 1 : 0;  // k-tiles of this wave (<= KPW)
-  const int rs = ktc * 128 + 8;                             // LDS row stride (halves)
+  const int nkt = kt_end - kt_begin;                       // k-tiles of this workgroup
+  const int kpw = wk < nkt ? (nkt - 1 - wk) / WK + 1 : 0;  // k-tiles of this wave (<= KPW)
+  const int rs = ktc * 128 + 8;                            // LDS row stride (halves)
   const DqK dk = dq_consts();
 
   // ---- activation slice: XPT chunks of 8 halves per thread --------------
@@ -67,16 +70,17 @@ __global__ __launch_bounds__(64 * WK) void gemv_kernel(
   const int cpr = ktc * 16;  // chunks per row
 #pragma unroll
   for (int r = 0; r < XPT; ++r) {
-    const int q = min(threadIdx.x + r * NTHREADS, M * cpr - 1);
+    const int q = min((int)threadIdx.x + r * NTHREADS, M * cpr - 1);
     const int m = q / cpr, kk = (q % cpr) * 8;
     const int k = min(kt_begin * 128 + kk, K - 8);  // halves past K are zeroed when stored
     xr[r] = ld_off<u32x4>(x, ((uint32_t)m * (uint32_t)K + (uint32_t)k) * 2u);
   }
 
   // ---- weights, zero words and scales of every k-tile of this wave ---------
+  // (one quantisation group per 128-row tile: G >= 128)
   u32x4 q[KPW][NTW];
-  uint32_t zw[KPW][NTW][GPT];
-  uint16_t sb[KPW][NTW][GPT];
+  uint32_t zw[KPW][NTW];
+  uint16_t sb[KPW][NTW];
   uint32_t woff[NTW], goff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
@@ -87,19 +91,15 @@ __global__ __launch_bounds__(64 * WK) void gemv_kernel(
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     // k-tiles past the wave's share reload its last one (no branch around loads)
-    const int kt = kt_begin + wave + WK * min(i, max(kpw - 1, 0));
+    const int kt = kt_begin + wk + WK * min(i, max(kpw - 1, 0));
     const int ktl = min(kt, KT - 1);
+    const uint32_t g = (uint32_t)min((ktl * 128) >> gshift, NG - 1);
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) q[i][j] = ld_off_nt<u32x4>(wt, woff[j] + (uint32_t)ktl * 1024u);
-#pragma unroll
-    for (int gg = 0; gg < GPT; ++gg) {
-      const uint32_t g = (uint32_t)min((ktl * 128 + 32 * BPG * gg) >> gshift, NG - 1);
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const uint32_t gi = goff[j] + g;
-        zw[i][j][gg] = ld_off<uint32_t>(z_r, gi * 8u + (uint32_t)(c >> 3) * 4u);
-        sb[i][j][gg] = ld_off<uint16_t>(s_r, (gi * 16u + c) * 2u);
-      }
+    for (int j = 0; j < NTW; ++j) {
+      q[i][j] = ld_off_nt<u32x4>(wt, woff[j] + (uint32_t)ktl * 1024u);
+      const uint32_t gi = goff[j] + g;
+      zw[i][j] = ld_off<uint32_t>(z_r, gi * 8u + (uint32_t)(c >> 3) * 4u);
+      sb[i][j] = ld_off<uint16_t>(s_r, (gi * 16u + c) * 2u);
     }
   }
 
@@ -117,67 +117,87 @@ __global__ __launch_bounds__(64 * WK) void gemv_kernel(
   __syncthreads();
 
   // ---- compute ---------------------------------------------------------------
-  f32x4 acc[NTW];
+  f32x4 acc[MT][NTW];
 #pragma unroll
-  for (int j = 0; j < NTW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int xrow = min(c, M - 1) * rs + lg * 8;
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + c, M - 1) * rs + lg * 8;
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     if (i < kpw) {
-      const int kl = (wave + WK * i) * 128;  // k offset inside the slice
+      const int kl = (wk + WK * i) * 128;  // k offset inside the slice
+      ZS zs[NTW];
 #pragma unroll
-      for (int gg = 0; gg < GPT; ++gg) {
-        ZS zs[NTW];
+      for (int j = 0; j < NTW; ++j) zs[j] = Dq<DT>::make((zw[i][j] >> (4 * (c & 7))) & 0xFu, sb[i][j]);
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) zs[j] = Dq<DT>::make((zw[i][j][gg] >> (4 * (c & 7))) & 0xFu, sb[i][j][gg]);
+      for (int w = 0; w < 4; ++w) {
+        V8 av[NTW];
 #pragma unroll
-        for (int b = 0; b < BPG; ++b) {
-          const int w = gg * BPG + b;
-          const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow + kl + 32 * w));
+        for (int j = 0; j < NTW; ++j) av[j] = Dq<DT>::word(q[i][j][w], zs[j], dk);
 #pragma unroll
-          for (int j = 0; j < NTW; ++j) acc[j] = mfma16x16x32(Dq<DT>::word(q[i][j][w], zs[j], dk), bx, acc[j]);
+        for (int mt = 0; mt < MT; ++mt) {
+          const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow[mt] + kl + 32 * w));
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
         }
       }
     }
   }
 
-  // ---- reduce the WK waves: thread t sums quad t of every wave ---------------
-  // quad (j, l) = column tile j, lane l: row l % 16, columns 4 (l / 16) + r.
-  constexpr int NQ = NTW * 64;
-  f32x4 res[(NQ + NTHREADS - 1) / NTHREADS];
+  // ---- reduce the WK waves: thread t sums quad t of every k-wave -------------
+  // quad index qd = ((wn * MT + mt) * NTW + j) * 64 + lane: m-tile mt, column
+  // tile wn*NTW + j, lane l: row 16 mt + l % 16, columns 4 (l / 16) + r.
+  constexpr int NQ = WN * MT * NTW * 64;
+  constexpr int QPT = (NQ + NTHREADS - 1) / NTHREADS;  // quads per thread
+  f32x4 res[QPT];
   if constexpr (WK > 1) {
     __syncthreads();  // every wave is done reading the activation slice
     f32x4* red = (f32x4*)smem;
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) red[(wave * NTW + j) * 64 + lane] = acc[j];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) red[wk * NQ + ((wn * MT + mt) * NTW + j) * 64 + lane] = acc[mt][j];
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < (NQ + NTHREADS - 1) / NTHREADS; ++u) {
+    for (int u = 0; u < QPT; ++u) {
       const int qd = min((int)threadIdx.x + u * NTHREADS, NQ - 1);
       f32x4 s4 = red[qd];
 #pragma unroll
       for (int o = 1; o < WK; ++o) s4 += red[o * NQ + qd];
       res[u] = s4;
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) res[j] = acc[j];
   }
 
-  // Quad u of this thread: tile j = qd / 64, lane l = qd % 64.
+  // Output quad of this thread: with WK > 1 thread t owns quads t + u*NTHREADS;
+  // with WK == 1 each lane keeps its own accumulators.
   auto quad_pos = [&](int u, int& m, int& n0) {
-    const int qd = threadIdx.x + u * NTHREADS;
-    const int l = qd & 63;
-    m = l & 15;
-    n0 = (nt0 + qd / 64) * 16 + 4 * (l >> 4);
+    int qd;
+    if constexpr (WK > 1) {
+      qd = threadIdx.x + u * NTHREADS;
+    } else {
+      const int mt = u / NTW, j = u % NTW;
+      qd = ((wn * MT + mt) * NTW + j) * 64 + lane;
+    }
+    const int l = qd & 63, t = qd >> 6;  // t = (wn' * MT + mt') * NTW + j'
+    const int j = t % NTW, mt = (t / NTW) % MT, wq = t / (NTW * MT);
+    m = mt * 16 + (l & 15);
+    n0 = (blockIdx.x * NTG + wq * NTW + j) * 16 + 4 * (l >> 4);
     return qd < NQ;
   };
+  auto quad_val = [&](int u) -> f32x4 {
+    if constexpr (WK > 1) return res[u];
+    else return acc[u / NTW][u % NTW];
+  };
+  constexpr int NU = WK > 1 ? QPT : MT * NTW;
 
   if (KS == 1) {
 #pragma unroll
-    for (int u = 0; u < (NQ + NTHREADS - 1) / NTHREADS; ++u) {
+    for (int u = 0; u < NU; ++u) {
       int m, n0;
-      if (quad_pos(u, m, n0) && m < M && n0 < N) store4<DT>(out, bias, m, N, n0, res[u]);
+      if (quad_pos(u, m, n0) && m < M && n0 < N) store4<DT>(out, bias, m, N, n0, quad_val(u));
     }
     return;
   }
@@ -186,12 +206,13 @@ __global__ __launch_bounds__(64 * WK) void gemv_kernel(
   const int64_t Np = (int64_t)NT * 16;
   float chk = 0.f;
 #pragma unroll
-  for (int u = 0; u < (NQ + NTHREADS - 1) / NTHREADS; ++u) {
+  for (int u = 0; u < NU; ++u) {
     int m, n0;
     if (quad_pos(u, m, n0) && m < M && n0 < Np) {
       float* p = part + ((int64_t)blockIdx.y * M + m) * Np + n0;
+      const f32x4 v = quad_val(u);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) chk += xchg_agent(p + r, res[u][r]);
+      for (int r = 0; r < 4; ++r) chk += xchg_agent(p + r, v[r]);
     }
   }
   // Consuming the returned values makes the wave wait until every exchange
@@ -206,7 +227,7 @@ __global__ __launch_bounds__(64 * WK) void gemv_kernel(
   __syncthreads();
   if (!s_last) return;
 #pragma unroll
-  for (int u = 0; u < (NQ + NTHREADS - 1) / NTHREADS; ++u) {
+  for (int u = 0; u < NU; ++u) {
     int m, n0;
     if (quad_pos(u, m, n0) && m < M && n0 < N) {
       f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -227,40 +248,42 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   using E = typename DT::elem;
   const uint16_t* sbase = (const uint16_t*)sr;
   const uint64_t* zbase = (const uint64_t*)zr;
-  const int ntw = p.variant / 1000, wk = (p.variant / 10) % 100, kpw = p.variant % 10;
-  const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
+  const int ntw = p.variant / 10000, wn = (p.variant / 1000) % 10, wk = (p.variant / 10) % 100, kpw = p.variant % 10;
+  const int mt = (int)((g.M + 15) / 16);
   const int xpt = p.xpt;
   dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
   const size_t lds = (size_t)p.lds_bytes;
-#define SGL_GEMV(NTW_, WK_, KPW_, XPT_, GPT_)                                                                       \
-  if (ntw == NTW_ && wk == WK_ && kpw == KPW_ && xpt == XPT_ && gpt == GPT_) {                                      \
-    hipLaunchKernelGGL((gemv_kernel<NTW_, WK_, KPW_, XPT_, GPT_, DT>), grid, dim3(64 * WK_), lds, s, (const E*)x,   \
-                       (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters, (int)g.M,     \
-                       (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);               \
-    return hipGetLastError();                                                                                      \
+#define SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, XPT_)                                                                  \
+  if (ntw == NTW_ && wn == WN_ && wk == WK_ && kpw == KPW_ && mt == MT_ && xpt == XPT_) {                          \
+    hipLaunchKernelGGL((gemv_kernel<NTW_, WN_, WK_, KPW_, MT_, XPT_, DT>), grid, dim3(64 * WN_ * WK_), lds, s,       \
+                       (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters,  \
+                       (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);      \
+    return hipGetLastError();                                                                                     \
   }
-#define SGL_GEMV_G(NTW_, WK_, KPW_, XPT_) \
-  SGL_GEMV(NTW_, WK_, KPW_, XPT_, 1) SGL_GEMV(NTW_, WK_, KPW_, XPT_, 2) SGL_GEMV(NTW_, WK_, KPW_, XPT_, 4)
-#define SGL_GEMV_X(NTW_, WK_, KPW_) SGL_GEMV_G(NTW_, WK_, KPW_, 1) SGL_GEMV_G(NTW_, WK_, KPW_, 2) \
-  SGL_GEMV_G(NTW_, WK_, KPW_, 4)
-  SGL_GEMV_X(1, 4, 4)
-  SGL_GEMV_X(1, 4, 8)
-  SGL_GEMV_X(1, 8, 4)
-  SGL_GEMV_X(2, 4, 4)
-  SGL_GEMV_X(2, 4, 8)
-  SGL_GEMV_X(2, 2, 8)
+#define SGL_GEMV_X(NTW_, WN_, WK_, KPW_, MT_) \
+  SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, 1) SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, 2) \
+  SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, 4) SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, 8)
+#define SGL_GEMV_M(NTW_, WN_, WK_, KPW_) SGL_GEMV_X(NTW_, WN_, WK_, KPW_, 1) SGL_GEMV_X(NTW_, WN_, WK_, KPW_, 2)
+  SGL_GEMV_M(1, 1, 4, 8)
+  SGL_GEMV_M(1, 1, 8, 4)
+  SGL_GEMV_M(2, 1, 4, 4)
+  SGL_GEMV_M(2, 2, 2, 8)
+  SGL_GEMV_M(2, 2, 4, 4)
+  SGL_GEMV_M(2, 4, 2, 4)
+  SGL_GEMV_M(2, 4, 4, 2)
+  SGL_GEMV_M(1, 4, 4, 4)
+#undef SGL_GEMV_M
 #undef SGL_GEMV_X
-#undef SGL_GEMV_G
 #undef SGL_GEMV
   return hipErrorInvalidValue;
 }
 
 }  // namespace
 
-// Variant code: ntw * 1000 + wk * 10 + kpw.
+// Variant code: ntw * 10000 + wn * 1000 + wk * 10 + kpw.
 bool gemv_variant_ok(int v) {
   switch (v) {
-    case 1044: case 1048: case 1084: case 2044: case 2048: case 2028:
+    case 11048: case 11084: case 21044: case 22028: case 22044: case 24024: case 24042: case 14044:
       return true;
     default:
       return false;

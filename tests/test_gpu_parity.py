@@ -330,23 +330,22 @@ def test_decode_bf16_variants(M, monkeypatch):
         assert ok, (variant, err, mx)
 
 
-@pytest.mark.parametrize("variant", [1044, 1048, 1084, 2044, 2048, 2028])
-@pytest.mark.parametrize("G", [128, 64, 32, -1])
+@pytest.mark.parametrize("variant", [11048, 11084, 21044, 22028, 22044, 24024, 24042, 14044])
+@pytest.mark.parametrize("G", [128, -1])
 def test_every_gemv_variant(variant, G, monkeypatch):
     """Each small-batch GEMV instantiation, with and without cross-workgroup
-    split-K, for every batch size it accepts (1..16 rows), on a K with a
-    partial last 128-row tile where G allows and N % 16 == 8."""
+    split-K, for batch sizes over both m-tile counts (1..32 rows), on a K with a
+    partial last 128-row tile and N % 16 == 8."""
     ops = _ops()
-    K = {32: 2336, 64: 2368, 128: 2432, -1: 2432}[G]
-    N = 200
-    t, d = _linear(K, N, G, seed=variant * 11 + (G if G > 0 else 7))
+    K, N = 2432, 200
+    t, d = _linear(K, N, G, seed=variant % 997 + (G if G > 0 else 7))
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
-    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "16")
+    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "32")
     monkeypatch.setenv("SGL_AWQ_GEMV_VARIANT", str(variant))
     for ks in (1, 3):
         monkeypatch.setenv("SGL_AWQ_GEMV_KS", str(ks))
-        for M in (1, 3, 4, 16):
+        for M in (1, 4, 16, 17, 32):
             x = oracle.make_activation(M, K, seed=M + ks)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
             ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
