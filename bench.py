@@ -15,10 +15,14 @@ linear moves K*N/2 (int4) + (K/128)*N/2 (zeros) + (K/128)*N*2 (scales)
 + 2*M*K (x) + 2*M*N (y) bytes.
 
 Also reported on the same line:
-  roofline      the decode kernel (skinny_kernel, every GEMM of the step): per
-                launch algorithmic bytes / average launch duration, measured
-                with HIP events around graphs of back-to-back launches on the
-                launch stream, against 8 TB/s HBM.
+  roofline      the dominant decode kernel of the step (the one with the most
+                time; ops.gemm_kernel names the kernel of each shape): algorithmic
+                bytes of its launches / their durations, measured with HIP events
+                around graphs of back-to-back launches on the launch stream,
+                against 8 TB/s HBM; `traffic` is its HBM bytes per launch from
+                the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
+                calibrated on a copy of known size; --pmc-workload/--pmc-summary).
+  decode_kernels  the same figures for every decode kernel of the step.
   per_m         the same per batch size.
   prefill       Llama-3-8B's four linears at M = 2048, TFLOP/s against the
                 2.5 PFLOP/s dense fp16 MFMA peak (MFMA-bound regime).
@@ -210,6 +214,111 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 30) -> dict:
                       f"4 linears at M=1,8,32, {passes} passes ({total_t:.1f} s); host {model}"}
 
 
+PMC_COPY_BYTES = 256 << 20
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_kernels_qwen3_4b_layer_hbm_traffic.md")
+
+
+def pmc_workload(ops, dev: torch.device, gen: torch.Generator) -> int:
+    """The step's decode GEMMs, each 4 times over 4 weight copies (one
+    dispatch per call, eagerly), then a 256 MiB device copy 3 times: the
+    calibration of the FETCH_SIZE / WRITE_SIZE counters."""
+    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in LAYER} for _ in range(4)]
+    cnts = {name: ops.make_counters(N, dev) for name, K, N in LAYER}
+    xg = torch.Generator(device=dev).manual_seed(1)
+    torch.cuda.synchronize()
+    for M in M_SET:
+        for name, K, N in LAYER:
+            x = torch.randn((M, K), generator=xg, device=dev).to(torch.float16)
+            out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            for c in range(4):
+                ops.gemm(x, reps[c][name], K, N, G, counters=cnts[name], out=out)
+    src = torch.empty(PMC_COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+    return 0
+
+
+def _pmc_rows(d: str):
+    import csv
+    import glob
+
+    path = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))[0]
+    return list(csv.DictReader(open(path)))
+
+
+def pmc_summary(fetch_dir: str, write_dir: str) -> str:
+    """Markdown summary of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) for the
+    decode kernels of --pmc-workload, each scaled by the counter's reading for
+    a device copy of known size (the copy reads and writes PMC_COPY_BYTES)."""
+    from collections import defaultdict
+
+    def per_kernel(d: str, counter: str):
+        vals = defaultdict(list)
+        for r in _pmc_rows(d):
+            if r["Counter_Name"] != counter:
+                continue
+            name = r["Kernel_Name"]
+            key = next((k for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel") if k in name), None)
+            if key is None and "copyBuffer" in name:  # torch's device-to-device copy is a runtime blit
+                key = "copy"
+            if key is not None:
+                vals[key].append(float(r["Counter_Value"]) * 1024.0)  # KiB -> bytes
+        return {k: sum(v) / len(v) for k, v in vals.items()}, {k: len(v) for k, v in vals.items()}
+
+    fetch, nf = per_kernel(fetch_dir, "FETCH_SIZE")
+    write, nw = per_kernel(write_dir, "WRITE_SIZE")
+    cf = PMC_COPY_BYTES / fetch["copy"]
+    cw = PMC_COPY_BYTES / write["copy"]
+    from sglite_amd import ops
+
+    algo = defaultdict(list)
+    for M in M_SET:
+        for _, K, N in LAYER:
+            algo[ops.gemm_kernel(M, N, K, G)].append(gemm_bytes(M, N, K))
+    lines = [
+        "# HBM traffic of the decode kernels (Qwen3-4B layer, M = 1, 8, 32), rocprofv3 PMC",
+        "",
+        "Commands (from the repository root, TMPDIR=/tmp), one counter per run:",
+        "`rocprofv3 --pmc FETCH_SIZE -f csv -d <fetch_dir> -o pmc -- python3 bench.py --pmc-workload`,",
+        "`rocprofv3 --pmc WRITE_SIZE -f csv -d <write_dir> -o pmc -- python3 bench.py --pmc-workload`,",
+        "`python3 bench.py --pmc-summary <fetch_dir> <write_dir>`.",
+        "",
+        f"Calibration: a {PMC_COPY_BYTES >> 20} MiB device copy reads FETCH_SIZE {fetch['copy'] / 1e6:.2f} MB and "
+        f"WRITE_SIZE {write['copy'] / 1e6:.2f} MB per dispatch, so the factors are {cf:.4f} (fetch) and "
+        f"{cw:.4f} (write).",
+        "",
+        "| kernel | dispatches | FETCH_SIZE (MB) | WRITE_SIZE (MB) | calibrated traffic (MB) | algorithmic (MB) |",
+        "|---|---|---|---|---|---|",
+    ]
+    for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel"):
+        if k not in fetch or k not in write:
+            continue
+        t = fetch[k] * cf + write[k] * cw
+        a = sum(algo[k]) / len(algo[k]) if algo[k] else float("nan")
+        lines.append(f"| `{k}` | {nf[k]} | {fetch[k] / 1e6:.3f} | {write[k] / 1e6:.3f} | {t / 1e6:.3f} | {a / 1e6:.3f} |")
+    lines.append("")
+    for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel"):
+        if k in fetch and k in write:
+            lines.append(f"traffic_bytes_per_launch {k} {int(fetch[k] * cf + write[k] * cw)}")
+    return "\n".join(lines) + "\n"
+
+
+def committed_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
+    try:
+        for line in open(PMC_SUMMARY):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def rocprof_summary(trace_dir: str, command: str) -> str:
     """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
 
@@ -226,25 +335,35 @@ def rocprof_summary(trace_dir: str, command: str) -> str:
     groups = defaultdict(list)
     for r in rows:
         name = r["Kernel_Name"]
-        if "skinny_kernel" not in name and "tiled_kernel" not in name:
+        if not any(k in name for k in ("skinny_kernel", "tiled_kernel", "gemv_kernel")):
             continue
         short = name.replace("(anonymous namespace)::", "").replace("sgl_awq::", "").replace("void ", "")
         short = short[:short.index("(")] if "(" in short else short
         key = (short, r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"])
         groups[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    n_lin = len(M_SET) * len(LAYER)
-    step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
-    sk = [d for (k, *_), ds in groups.items() if k.startswith("skinny") for d in ds]
-    mean_us = sum(sk) / len(sk)
-    mean_b = step_bytes / n_lin
+    from sglite_amd import ops
+
     lines = [
-        "# Decode kernel (skinny_kernel) on the Qwen3-4B layer workload, rocprofv3 kernel trace",
+        "# Decode kernels on the Qwen3-4B layer workload (M = 1, 8, 32), rocprofv3 kernel trace",
         "",
         f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
         "",
-        f"skinny_kernel dispatches: {len(sk)}, mean duration {mean_us:.3f} us; mean algorithmic bytes per "
-        f"launch {mean_b / 1e6:.3f} MB (step bytes {step_bytes} / {n_lin} launches); "
-        f"achieved {mean_b / mean_us / 1e3:.1f} GB/s = {mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.",
+        "Every (M, linear) of the step is launched equally often, so a kernel's mean algorithmic bytes per",
+        "launch is the mean over the (M, linear) pairs it serves.",
+        "",
+    ]
+    for kern in ("skinny_kernel", "gemv_kernel"):
+        pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.gemm_kernel(M, N, K, G) == kern]
+        ds = [d for (k, *_), v in groups.items() if k.startswith(kern.split("_")[0]) for d in v]
+        if not pairs or not ds:
+            continue
+        mean_b = sum(gemm_bytes(*p) for p in pairs) / len(pairs)
+        mean_us = sum(ds) / len(ds)
+        lines.append(f"* `{kern}`: {len(pairs)} of the step's {len(M_SET) * len(LAYER)} launches; "
+                     f"{len(ds)} dispatches, mean duration {mean_us:.3f} us; mean algorithmic bytes "
+                     f"{mean_b / 1e6:.3f} MB; achieved {mean_b / mean_us / 1e3:.1f} GB/s = "
+                     f"{mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.")
+    lines += [
         "",
         "| kernel | grid (x, y) | block | dispatches | mean us | min us | max us |",
         "|---|---|---|---|---|---|---|",
@@ -268,9 +387,16 @@ def main() -> int:
                     help="print a markdown summary of a rocprofv3 --kernel-trace run of this script and exit")
     ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
                                                   "python3 bench.py --steps 500 --no-cpu-baseline")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print a markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --pmc-workload")
     args = ap.parse_args()
     if args.rocprof_summary:
         print(rocprof_summary(args.rocprof_summary, args.rocprof_command), end="")
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary), end="")
         return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
@@ -284,6 +410,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(0)
+    if args.pmc_workload:
+        return pmc_workload(ops, dev, gen)
     C = args.copies
     reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in LAYER} for _ in range(C)]
     cnts = [{name: ops.make_counters(N, dev) for name, K, N in LAYER} for _ in range(C)]
@@ -312,7 +440,7 @@ def main() -> int:
 
     # Per-launch durations of the decode kernel: graphs of C back-to-back
     # launches of one (M, linear) over the C weight copies.
-    per_m, kb, kt = {}, 0, 0.0
+    per_m, per_kernel = {}, {}
     for M in M_SET:
         mb, mt, lin = 0, 0.0, {}
         for name, K, N in LAYER:
@@ -323,19 +451,27 @@ def main() -> int:
             time_replays([g], 2)
             us = time_replays([g], 5) * 1e3 / (5 * C)
             b = gemm_bytes(M, N, K)
-            lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1)}
+            kern = ops.gemm_kernel(M, N, K, G)
+            lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1), "kernel": kern}
+            acc = per_kernel.setdefault(kern, {"launches": 0, "bytes": 0, "us": 0.0})
+            acc["launches"] += 1
+            acc["bytes"] += b
+            acc["us"] += us
             mb += b
             mt += us
             del g
         per_m[str(M)] = {"GB/s": round(mb / mt / 1e3, 1), "us_per_layer": round(mt, 3), "linears": lin}
-        kb += mb
-        kt += mt
-    achieved = kb / kt / 1e3
+    # The dominant kernel is the one with the most time in the step.
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
+    d = per_kernel[dom]
+    achieved = d["bytes"] / d["us"] / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "skinny_kernel (decode split-K W4A16)",
-                "bytes_per_launch_avg": kb // (len(M_SET) * len(LAYER)),
-                "us_per_launch_avg": round(kt / (len(M_SET) * len(LAYER)), 3)}
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dom),
+                "kernel": dom, "launches_per_step": d["launches"],
+                "bytes_per_launch_avg": d["bytes"] // d["launches"],
+                "us_per_launch_avg": round(d["us"] / d["launches"], 3)}
+    kernels = {k: {"launches_per_step": v["launches"], "GB/s": round(v["bytes"] / v["us"] / 1e3, 1),
+                   "us_per_step": round(v["us"], 3)} for k, v in per_kernel.items()}
     del steps
     torch.cuda.synchronize()
 
@@ -393,6 +529,7 @@ def main() -> int:
                    "weight_copies": C, "weight_bytes_rotated": C * sum(gemm_bytes(0, N, K) for _, K, N in LAYER),
                    "step_bytes": step_bytes},
         "roofline": roofline,
+        "decode_kernels": kernels,
         "per_m": per_m,
         "prefill": prefill,
         "moe": moe,

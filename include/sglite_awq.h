@@ -97,6 +97,10 @@ int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype,
  * every call leaves them zero again.  Calls sharing `counters` must not run
  * concurrently (use one counters buffer per stream). */
 int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G);
+/* Which kernel awq_w4a16_gemm runs for this shape: 0 = decode split-K kernel,
+ * 1 = tiled MFMA kernel, 2 = small-batch GEMV kernel (benchmarks and
+ * diagnostics; no counterpart in the reference). */
+int awq_gemm_kernel_kind(int64_t M, int64_t N, int64_t K, int64_t G);
 int64_t awq_counter_bytes(int64_t N);
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype,

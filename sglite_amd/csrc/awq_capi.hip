@@ -160,6 +160,14 @@ int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G) {
   return plan_gemm(make_geom(M, N, K, Gr)).ws_bytes;
 }
 
+int awq_gemm_kernel_kind(int64_t M, int64_t N, int64_t K, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be positive");
+  return plan_gemm(make_geom(M, N, K, Gr)).kind;
+}
+
 int64_t awq_counter_bytes(int64_t N) {
   if (N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "N must be positive");
   return ((N + 15) / 16) * 4;

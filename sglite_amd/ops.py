@@ -147,6 +147,15 @@ def workspace_bytes(M: int, N: int, K: int, group_size: int) -> int:
     return _lib.check(_lib.load().awq_workspace_bytes(M, N, K, G), "awq_workspace_bytes")
 
 
+KERNEL_NAMES = {0: "skinny_kernel", 1: "tiled_kernel", 2: "gemv_kernel"}
+
+
+def gemm_kernel(M: int, N: int, K: int, group_size: int) -> str:
+    """Name of the kernel ``gemm`` runs for this shape."""
+    G = resolve_group_size(group_size, K)
+    return KERNEL_NAMES[_lib.check(_lib.load().awq_gemm_kernel_kind(M, N, K, G), "awq_gemm_kernel_kind")]
+
+
 def make_counters(N: int, device: torch.device) -> torch.Tensor:
     """Split-K arrival counters: zeroed once here, left zeroed by every GEMM call."""
     nbytes = _lib.check(_lib.load().awq_counter_bytes(N), "awq_counter_bytes")
