@@ -50,8 +50,9 @@ int check_shape(int64_t K, int64_t N, int64_t G, int dtype, int64_t* G_out) {
     return fail(AWQ_STATUS_INVALID_ARGUMENT, "dtype must be AWQ_DTYPE_FP16 (0) or AWQ_DTYPE_BF16 (1), got %d", dtype);
   if (K <= 0 || N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "K and N must be positive (K=%lld, N=%lld)",
                                     (long long)K, (long long)N);
-  if (K > (int64_t(1) << 30) || N > (int64_t(1) << 30))
-    return fail(AWQ_STATUS_UNSUPPORTED, "K and N must be below 2^30 (K=%lld, N=%lld)", (long long)K, (long long)N);
+  if (K >= (int64_t(1) << 24) || N >= (int64_t(1) << 30))
+    return fail(AWQ_STATUS_UNSUPPORTED, "K must be below 2^24 and N below 2^30 (K=%lld, N=%lld)", (long long)K,
+                (long long)N);
   const int64_t Gr = (G == -1) ? K : G;
   if (!(Gr == 32 || Gr == 64 || Gr == 128 || Gr == K))
     return fail(AWQ_STATUS_INVALID_ARGUMENT, "group size must be -1, 32, 64, 128 or K, got %lld", (long long)G);

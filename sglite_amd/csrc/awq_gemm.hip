@@ -1,16 +1,11 @@
-// W4A16 GEMM kernels for gfx950: out[M, N] = x[M, K] @ W (+ bias), fp32 accumulation.
+// W4A16 GEMM planning and dispatch for gfx950: out[M, N] = x[M, K] @ W
+// (+ bias), fp32 accumulation.  Three kernels share the CDNA4 tile layout
+// (awq_device.h):
 //
-// Two kernels share the CDNA4 tile layout (awq_device.h):
-//
-//  * skinny_kernel (decode, M <= 32, awq_skinny.hip): HBM-bound split-K
-//    kernel, one launch per linear.
-//
-//  * tiled_kernel (prefill, M > 32): MFMA-bound.  A workgroup computes
-//    BM x 256 outputs; the activation tile (BM x 128 per k-step) is staged
-//    through double-buffered LDS in MFMA-fragment order (conflict-free 16-byte
-//    reads), and each wave dequantises the weights of its own 64 columns
-//    straight from global memory into MFMA operands (no LDS round trip, no
-//    redundant dequantisation across waves).
+//  * gemv_kernel (awq_gemv.hip): batches of a few rows, HBM-bound;
+//  * skinny_kernel (awq_skinny.hip): decode batches up to 32 rows, HBM-bound
+//    split-K;
+//  * tiled_kernel (awq_tiled.hip): prefill, MFMA-bound.
 //
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
@@ -27,128 +22,6 @@
 namespace sgl_awq {
 
 namespace {
-
-// ---------------------------------------------------------------------------
-// Tiled MFMA kernel: BM x 256 per workgroup, 4 waves of BM x 64.
-// ---------------------------------------------------------------------------
-template <int BM, typename DT>
-__global__ __launch_bounds__(256) void tiled_kernel(const typename DT::elem* __restrict__ x,
-                                                    const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
-                                                    const uint64_t* __restrict__ z_r,
-                                                    const typename DT::elem* __restrict__ bias,
-                                                    typename DT::elem* __restrict__ out, int M, int N, int K, int NT,
-                                                    int KT, int NG, int gshift) {
-  using E = typename DT::elem;
-  using V8 = typename DT::vec8;
-  using ZS = typename Dq<DT>::ZS;
-  constexpr int MTL = BM / 16;
-  constexpr int NTW = 4;
-  // [buffer][m-tile][k-block][lane] -> 16 bytes: one MFMA B operand per (mt, kb)
-  __shared__ u32x4 xs[2][MTL * 4 * 64];
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = lane & 15, lg = lane >> 4;
-  const int nt0 = blockIdx.x * 16 + wave * NTW;
-  const DqK dk = dq_consts();
-  const int64_t m0 = (int64_t)blockIdx.y * BM;
-
-  f32x4 acc[MTL][NTW];
-#pragma unroll
-  for (int mt = 0; mt < MTL; ++mt)
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Loader: thread (wave, lane) fetches fragment (mt = i, kb = wave) of the
-  // activation tile for i = 0..MTL-1.
-  const E* xsrc[MTL];  // row starts (rows past M clamp to M - 1 and are zeroed)
-  bool xval[MTL];
-#pragma unroll
-  for (int i = 0; i < MTL; ++i) {
-    const int64_t m = m0 + i * 16 + c;
-    xval[i] = m < M;
-    xsrc[i] = x + min(m, (int64_t)M - 1) * K;
-  }
-  int ntc[NTW];
-  const u32x4* wbase[NTW];
-#pragma unroll
-  for (int j = 0; j < NTW; ++j) {
-    ntc[j] = min(nt0 + j, NT - 1);
-    wbase[j] = wt + (int64_t)ntc[j] * KT * 64 + lane;
-  }
-
-  u32x4 xr[MTL];
-  u32x4 q[NTW], qn[NTW];
-  auto load_x = [&](int kt) {
-    // k-blocks past K (K % 128 != 0) read the row's first 16 bytes and are zeroed.
-    const bool kval = kt * 128 + wave * 32 < K;
-    const int64_t koff = kval ? (int64_t)kt * 128 + wave * 32 + lg * 8 : 0;
-#pragma unroll
-    for (int i = 0; i < MTL; ++i) {
-      const u32x4 v = *(const u32x4*)(xsrc[i] + koff);
-      xr[i] = (xval[i] && kval) ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < MTL; ++i) xs[buf][(i * 4 + wave) * 64 + lane] = xr[i];
-  };
-
-  load_x(0);
-#pragma unroll
-  for (int j = 0; j < NTW; ++j) q[j] = wbase[j][0];
-  store_x(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      load_x(kt + 1);
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) qn[j] = wbase[j][(int64_t)(kt + 1) * 64];
-    }
-    int gprev = -1;
-    ZS zs[NTW];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int kb = kt * 128 + 32 * w;
-      if (kb >= K) break;
-      const int g = kb >> gshift;
-      if (g != gprev) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          const int64_t gi = (int64_t)ntc[j] * NG + g;
-          zs[j] = Dq<DT>::make(zero_nibble(z_r[gi], c), s_r[gi * 16 + c]);
-        }
-        gprev = g;
-      }
-      V8 a[NTW];
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) a[j] = Dq<DT>::word(q[j][w], zs[j], dk);
-#pragma unroll
-      for (int mt = 0; mt < MTL; ++mt) {
-        const V8 b = __builtin_bit_cast(V8, xs[cur][(mt * 4 + w) * 64 + lane]);
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(a[j], b, acc[mt][j]);
-      }
-    }
-    if (more) {
-      store_x(cur ^ 1);
-#pragma unroll
-      for (int j = 0; j < NTW; ++j) q[j] = qn[j];
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MTL; ++mt)
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) {
-      const int64_t m = m0 + mt * 16 + c;
-      const int n0 = (nt0 + j) * 16 + 4 * lg;
-      if (m < M && n0 < N) store4<DT>(out, bias, m, N, n0, acc[mt][j]);
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Planning and dispatch.
@@ -169,27 +42,6 @@ bool skinny_variant_ok(int v) {
     default:
       return false;
   }
-}
-
-template <typename DT>
-hipError_t launch_tiled_dt(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                           const void* bias, void* out, const Geom& g, hipStream_t s) {
-  using E = typename DT::elem;
-  const uint16_t* sbase = (const uint16_t*)sr;
-  const uint64_t* zbase = (const uint64_t*)zr;
-  dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
-#define SGL_TILED(BM_)                                                                                          \
-  if (p.variant == BM_) {                                                                                     \
-    hipLaunchKernelGGL((tiled_kernel<BM_, DT>), grid, dim3(256), 0, s, (const E*)x, (const u32x4*)w, sbase, zbase, \
-                       (const E*)bias, (E*)out, (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG,  \
-                       g.gshift);                                                                             \
-    return hipGetLastError();                                                                                 \
-  }
-  SGL_TILED(64)
-  SGL_TILED(128)
-  SGL_TILED(256)
-#undef SGL_TILED
-  return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -300,7 +152,8 @@ GemmPlan plan_gemm(const Geom& g) {
     p.kind = 1;
     int bm = g.M <= 64 ? 64 : 128;
     const int env = env_int("SGL_AWQ_TILED_BM", 0);
-    if (env == 64 || env == 128 || env == 256) bm = env;
+    if (env == 64 || env == 128) bm = env;
+    if (g.K > tiled_max_k(bm)) bm = 64;
     p.variant = bm;
     p.grid_x = (g.NT + 15) / 16;
     p.grid_y = (g.M + bm - 1) / bm;
@@ -316,8 +169,7 @@ hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const vo
                        hipStream_t s) {
   if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
   if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
-  return dtype == 0 ? launch_tiled_dt<F16>(p, x, w, sr, zr, bias, out, g, s)
-                    : launch_tiled_dt<BF16>(p, x, w, sr, zr, bias, out, g, s);
+  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, s);
 }
 
 }  // namespace sgl_awq

@@ -43,6 +43,9 @@ bool gemv_variant_ok(int v);
 hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);
+int64_t tiled_max_k(int bm);
+hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                        const void* bias, void* out, int dtype, const Geom& g, hipStream_t s);
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);

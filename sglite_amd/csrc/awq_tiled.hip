@@ -1,0 +1,321 @@
+// Prefill W4A16 GEMM (M > 32): MFMA-bound tiled kernel for gfx950.
+//
+// A workgroup of 4 waves computes BM x 256 outputs; wave w owns the 64 output
+// columns of four 16-column weight tiles and all BM rows, so every packed
+// weight word is dequantised exactly once per workgroup, straight from
+// registers into MFMA operands.  The k loop runs over 128-row k-tiles with NS
+// pipeline stages; stage p holds one k-tile's weights, zero points and scales
+// in registers and its activation tile (BM x 128) in LDS buffer p:
+//
+//   * activation tiles go global -> LDS directly (buffer loads with the LDS
+//     destination, no registers), stored in MFMA-fragment order so every
+//     operand read is one conflict-free 16-byte LDS read.  Rows past M clamp
+//     to a valid row (their outputs are never stored); k-blocks past K are
+//     read through a zero-length buffer, which returns zeros without touching
+//     memory;
+//   * weights, zero points and scales go to registers; their offsets advance
+//     in scalar registers (the buffer-load SGPR offset), so no load costs
+//     vector ALU work;
+//   * a k-tile's loads are issued NS - 1 steps before it is computed,
+//     activations first.  The vector-memory counter retires in issue order,
+//     so the end of each step waits for exactly the loads older than the
+//     next k-tile's activations (a count fixed at compile time) and then
+//     meets the other waves at a barrier that carries no memory fence (a
+//     fenced barrier would also wait for the activation loads just issued);
+//   * each k-tile's four 32-row blocks are software-pipelined: block w's MFMAs
+//     run while block w + 1 is dequantised into the other operand buffer.
+//
+// Workgroups are numbered XCD-aware: the hardware deals consecutive
+// workgroup ids round-robin over the 8 XCDs, and the id -> tile map makes the
+// workgroups that one XCD runs together cover a compact patch of 4 row blocks
+// x 8 column blocks, so that XCD's L2 serves the shared activation and weight
+// tiles.
+//
+// Replaces awq_gemm_kernel / awq_gemm_triton
+// (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
+// and gptq_marlin_gemm (marlin_utils.py:388-410) for large batches.
+#include "awq_device.h"
+#include "awq_epilogue.h"
+#include "awq_launch.h"
+
+namespace sgl_awq {
+
+namespace {
+
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// One 16-byte buffer load per lane straight into LDS: lane l's bytes land at
+// dst + 16 * l (dst is wave-uniform).
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory loads are
+// outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+struct TiledArgs {
+  const void* x;
+  const u32x4* w;
+  const uint16_t* s;
+  const uint64_t* z;
+  const void* bias;
+  void* out;
+  int M, N, K, NT, KT, NG, gshift;
+  int gx, gy;  // column blocks (256 columns), row blocks (BM rows)
+};
+
+// Workgroup id -> (column block, row block).  Ids b, b + 8, b + 16, ... run
+// on one XCD; they are given consecutive logical indices, and logical
+// indices walk groups of up to 4 row blocks column-major.
+__device__ __forceinline__ void tile_of(int b, int gx, int gy, int& bx, int& by) {
+  const int total = gx * gy;
+  const int per = total >> 3, rem = total & 7;
+  const int xcd = b & 7, idx = b >> 3;
+  const int L = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
+  const int band = 4 * gx;                // logical indices per group of 4 row blocks
+  const int grp = L / band;
+  const int rows = min(4, gy - grp * 4);  // row blocks in this group
+  const int r = L - grp * band;
+  bx = r / rows;
+  by = grp * 4 + r % rows;
+}
+
+template <int GPT>
+struct WStage {
+  u32x4 q[4];          // one 16-byte weight vector per column tile
+  uint32_t z[4][GPT];  // the zero-point word holding this lane's nibble, per group
+  uint16_t s[4][GPT];  // this lane's column scale, per group
+};
+
+template <int BM, int GPT, int NS, typename DT>
+__global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
+  using E = typename DT::elem;
+  using V8 = typename DT::vec8;
+  using ZS = typename Dq<DT>::ZS;
+  constexpr int MTL = BM / 16;
+  constexpr int NTW = 4;
+  constexpr int XS = MTL * 4 * 64;              // 16-byte slots per activation buffer
+  constexpr int kLoadsW = NTW * (1 + 2 * GPT);  // load instructions per weight stage
+  // Loads issued after a k-tile's activations, up to the end of the step
+  // before that k-tile: its own weights and the NS - 2 k-tiles behind it.
+  constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * MTL;
+  static_assert(kAfterX < 64, "vector-memory counter range");
+  // One activation buffer per stage, as separate objects: the compiler then
+  // knows which LDS loads an outstanding LDS-destination load can affect.
+  // [m-tile * 4 + k-block][lane] -> one MFMA B operand (16 bytes)
+  __shared__ u32x4 xs0[XS];
+  __shared__ u32x4 xs1[XS];
+  __shared__ u32x4 xs2[NS > 2 ? XS : 1];
+  auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : xs2); };
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, lg = lane >> 4;
+  int bx, by;
+  tile_of(blockIdx.x, a.gx, a.gy, bx, by);
+  const int m0 = by * BM;
+  const int rows = min(BM, a.M - m0);
+  const int K = a.K, KT = a.KT, NG = a.NG;
+  const DqK dk = dq_consts();
+
+  // Activations: this workgroup's rows; thread (wave, lane) loads fragment
+  // (m-tile i, k-block wave) of each k-tile.
+  const E* xb = (const E*)a.x + (int64_t)m0 * K;
+  const uint32_t xbytes = (uint32_t)rows * (uint32_t)K * 2u;
+  uint32_t xoff[MTL];
+#pragma unroll
+  for (int i = 0; i < MTL; ++i)
+    xoff[i] = (uint32_t)min(i * 16 + c, rows - 1) * (uint32_t)K * 2u + (uint32_t)(wave * 64 + lg * 16);
+
+  // Weights, zeros and scales of this wave's four column tiles (the last
+  // ones clamp to the final tile; their columns are never stored).
+  const int nt0 = bx * 16 + wave * NTW;
+  const int ntb = min(nt0, a.NT - 1);
+  const u32x4* wb = a.w + (int64_t)ntb * KT * 64;
+  const uint64_t* zb = a.z + (int64_t)ntb * NG;
+  const uint16_t* sb = a.s + (int64_t)ntb * NG * 16;
+  // Buffer ranges end at the wave's last real tile, so the reads of groups
+  // past K in a partial last k-tile (G < 128) return zeros.
+  const uint32_t ntiles = (uint32_t)min(NTW, a.NT - ntb);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ntiles * (uint32_t)KT * 1024u);
+  const __amdgpu_buffer_rsrc_t zr = make_rsrc(zb, ntiles * (uint32_t)NG * 8u);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(sb, ntiles * (uint32_t)NG * 32u);
+  uint32_t woff[NTW], zoff[NTW], soff[NTW];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    const uint32_t dt = (uint32_t)(min(nt0 + j, a.NT - 1) - ntb);
+    woff[j] = dt * (uint32_t)KT * 1024u + (uint32_t)lane * 16u;
+    zoff[j] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
+    soff[j] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+  }
+  const uint32_t zshift = 4u * (uint32_t)(c & 7);
+
+  f32x4 acc[MTL][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MTL; ++mt)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Activation k-tile kt (zeros past K) into LDS buffer p.
+  auto load_x = [&](int p, int kt) {
+    const bool kval = kt * 128 + wave * 32 < K;  // wave-uniform
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
+    u32x4* dst = xbuf(p);
+#pragma unroll
+    for (int i = 0; i < MTL; ++i)
+      load_lds16(r, &dst[(i * 4 + wave) * 64], xoff[i], kt * 256);
+  };
+  auto load_w = [&](WStage<GPT>& S, int kt) {
+    const int g0 = (kt * 128) >> a.gshift;  // first group of the k-tile
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      S.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kt * 1024, 0);
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j] + 8 * g, g0 * 8, 0);
+#pragma unroll
+      for (int g = 0; g < GPT; ++g)
+        S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j] + 32 * g, g0 * 32, 0);
+    }
+  };
+  auto compute = [&](const WStage<GPT>& S, const u32x4* xsb) {
+    ZS zs[NTW][GPT];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) zs[j][g] = Dq<DT>::make((S.z[j][g] >> zshift) & 0xFu, S.s[j][g]);
+    // Block w's MFMAs run while block w + 1 is dequantised (double-buffered
+    // operands); the fence keeps the scheduler from mixing blocks, which
+    // would rename accumulators and cost register copies.
+    V8 av[2][NTW];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) av[0][j] = Dq<DT>::word(S.q[j][0], zs[j][0], dk);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w < 3) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) av[(w + 1) & 1][j] = Dq<DT>::word(S.q[j][w + 1], zs[j][(w + 1) * GPT / 4], dk);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MTL; ++mt) {
+        const V8 b = __builtin_bit_cast(V8, xsb[(mt * 4 + w) * 64 + lane]);
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[w & 1][j], b, acc[mt][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Every wave's activation loads of the next k-tile have landed, and every
+  // wave is done reading the buffer the next step refills.
+  auto sync_step = [&]() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterX));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  WStage<GPT> st[NS];
+  // Stage p: issue k-tile kt + NS - 1 into stage p - 1, compute k-tile kt.
+  auto step = [&](int p, int kt) {
+    const int pa = (p + NS - 1) % NS;
+    load_x(pa, kt + NS - 1);
+    __builtin_amdgcn_sched_barrier(0);  // the wait counts rely on this issue order
+    load_w(st[pa], min(kt + NS - 1, KT - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(st[p], xbuf(p));
+    sync_step();
+  };
+
+#pragma unroll
+  for (int p = 0; p + 1 < NS; ++p) {
+    load_x(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(st[p], min(p, KT - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  sync_step();
+
+  // Whole rounds of NS k-tiles, then the remaining k-tiles.  A counted loop
+  // keeps every step's loads unconditional, so the compiler's wait counts
+  // see the true prefetch distance.
+  int kt = 0;
+  for (; kt + NS <= KT; kt += NS) {
+#pragma unroll
+    for (int p = 0; p < NS; ++p) step(p, kt + p);
+  }
+#pragma unroll
+  for (int p = 0; p + 1 < NS; ++p)
+    if (kt + p < KT) step(p, kt + p);
+
+  // The last steps prefetched past the end; no load may still be writing
+  // this workgroup's LDS when it exits.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  const E* bias = (const E*)a.bias;
+  E* out = (E*)a.out;
+#pragma unroll
+  for (int mt = 0; mt < MTL; ++mt)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int m = mt * 16 + c;
+      const int n0 = (nt0 + j) * 16 + 4 * lg;
+      if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, acc[mt][j]);
+    }
+}
+
+template <int BM, typename DT>
+hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
+  const dim3 grid((unsigned)(a.gx * a.gy)), block(256);
+  switch (gpt) {
+    case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, 3, DT>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((tiled_kernel<BM, 2, 3, DT>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((tiled_kernel<BM, 4, 2, DT>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename DT>
+hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t s) {
+  switch (p.variant) {
+    case 64: return launch_bm<64, DT>(a, gpt, s);
+    case 128: return launch_bm<128, DT>(a, gpt, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+// Largest K the prefill kernel takes at row block bm: its per-workgroup
+// activation offsets (bm rows of K elements) stay below 2^31 bytes.
+int64_t tiled_max_k(int bm) { return ((int64_t(1) << 31) - 1) / (2 * (int64_t)bm); }
+
+hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                        const void* bias, void* out, int dtype, const Geom& g, hipStream_t s) {
+  if (p.grid_x * p.grid_y >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
+  TiledArgs a;
+  a.x = x;
+  a.w = (const u32x4*)w;
+  a.s = (const uint16_t*)sr;
+  a.z = (const uint64_t*)zr;
+  a.bias = bias;
+  a.out = out;
+  a.M = (int)g.M;
+  a.N = (int)g.N;
+  a.K = (int)g.K;
+  a.NT = (int)g.NT;
+  a.KT = (int)g.KT;
+  a.NG = (int)g.NG;
+  a.gshift = g.gshift;
+  a.gx = (int)p.grid_x;
+  a.gy = (int)p.grid_y;
+  // Groups per 128-row k-tile: 1 for G >= 128 (or one group), else 128 / G.
+  const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
+  return dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
+}
+
+}  // namespace sgl_awq

@@ -367,3 +367,27 @@ def test_gemv_bf16_and_bias(M):
     y = ops.gemm(x.to(DEV), r, K, N, G, bias=bias.to(DEV), counters=cnt)
     ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
     assert ok, (err, mx)
+
+
+@pytest.mark.parametrize("bm", [64, 128])
+@pytest.mark.parametrize("G", [32, 64, 128, -1])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_every_tiled_variant(bm, G, dtype, monkeypatch):
+    """Each prefill-kernel instantiation (row block x groups per 128-row
+    k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
+    past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
+    leave the last row block partial; pipelines of 2 and 3 stages, whole
+    rounds plus a remainder."""
+    ops = _ops()
+    K = {32: 2336, 64: 2368, 128: 2432, -1: 1120}[G]
+    N = 264
+    t, d = _linear(K, N, G, seed=bm + (G if G > 0 else 5), dtype=dtype)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    monkeypatch.setenv("SGL_AWQ_TILED_BM", str(bm))
+    for M in (33, 130, 257):
+        x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
+        y = ops.gemm(x.to(DEV), r, K, N, G)
+        ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+        ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+        assert ok, (bm, G, M, err, mx)
+    assert ops.gemm_kernel(130, N, K, G) == "tiled_kernel"
