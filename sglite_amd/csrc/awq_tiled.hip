@@ -112,7 +112,8 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   __shared__ u32x4 xs0[XS];
   __shared__ u32x4 xs1[XS];
   __shared__ u32x4 xs2[NS > 2 ? XS : 1];
-  auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : xs2); };
+  __shared__ u32x4 xs3[NS > 3 ? XS : 1];
+  auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : xs3)); };
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -162,14 +163,13 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Activation k-tile kt (zeros past K) into LDS buffer p.
-  auto load_x = [&](int p, int kt) {
+  // Activation k-tile kt (zeros past K), m-tiles [i0, i1), into LDS buffer p.
+  auto load_x = [&](int p, int kt, int i0, int i1) {
     const bool kval = kt * 128 + wave * 32 < K;  // wave-uniform
     const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
     u32x4* dst = xbuf(p);
 #pragma unroll
-    for (int i = 0; i < MTL; ++i)
-      load_lds16(r, &dst[(i * 4 + wave) * 64], xoff[i], kt * 256);
+    for (int i = i0; i < i1; ++i) load_lds16(r, &dst[(i * 4 + wave) * 64], xoff[i], kt * 256);
   };
   auto load_w = [&](WStage<GPT>& S, int kt) {
     const int g0 = (kt * 128) >> a.gshift;  // first group of the k-tile
@@ -183,61 +183,87 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
         S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j] + 32 * g, g0 * 32, 0);
     }
   };
-  auto compute = [&](const WStage<GPT>& S, const u32x4* xsb) {
-    ZS zs[NTW][GPT];
+
+  WStage<GPT> st[NS];
+  ZS zs[NTW][GPT];  // dequantisation constants of the k-tile being computed
+  V8 av[2][NTW];    // dequantised weights of the current and the next 32-row block
+  V8 bf[2][MTL];    // activation fragments of the current and the next block
+  auto make_zs = [&](const WStage<GPT>& S) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j)
 #pragma unroll
       for (int g = 0; g < GPT; ++g) zs[j][g] = Dq<DT>::make((S.z[j][g] >> zshift) & 0xFu, S.s[j][g]);
-    // Block w's MFMAs run while block w + 1 is dequantised (double-buffered
-    // operands); the fence keeps the scheduler from mixing blocks, which
-    // would rename accumulators and cost register copies.
-    V8 av[2][NTW];
-#pragma unroll
-    for (int j = 0; j < NTW; ++j) av[0][j] = Dq<DT>::word(S.q[j][0], zs[j][0], dk);
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      if (w < 3) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) av[(w + 1) & 1][j] = Dq<DT>::word(S.q[j][w + 1], zs[j][(w + 1) * GPT / 4], dk);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MTL; ++mt) {
-        const V8 b = __builtin_bit_cast(V8, xsb[(mt * 4 + w) * 64 + lane]);
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[w & 1][j], b, acc[mt][j]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
   };
-  // Every wave's activation loads of the next k-tile have landed, and every
-  // wave is done reading the buffer the next step refills.
+  // Operands of block w of a k-tile into buffer slot `slot`.
+  auto fetch = [&](int slot, const WStage<GPT>& S, const u32x4* xsb, int w) {
+#pragma unroll
+    for (int mt = 0; mt < MTL; ++mt) bf[slot][mt] = __builtin_bit_cast(V8, xsb[(mt * 4 + w) * 64 + lane]);
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) av[slot][j] = Dq<DT>::word(S.q[j][w], zs[j][w * GPT / 4], dk);
+  };
+  // The MFMAs of one block, with the LDS reads and dequantisation of the
+  // next block spread between them (one LDS read, then four MFMAs each
+  // followed by up to two VALU operations, per m-tile).
+  auto mma = [&](int slot) {
+#pragma unroll
+    for (int mt = 0; mt < MTL; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[slot][j], bf[slot][mt], acc[mt][j]);
+#pragma unroll
+    for (int i = 0; i < MTL; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+#pragma unroll
+      for (int r = 0; r < NTW; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Every wave's activation loads of k-tile kt + 1 have landed, and every
+  // wave is done reading the buffer that the next activation load refills.
   auto sync_step = [&]() {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterX));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
-  WStage<GPT> st[NS];
-  // Stage p: issue k-tile kt + NS - 1 into stage p - 1, compute k-tile kt.
+  // One k-tile.  Stage p holds k-tile kt; k-tile kt + NS - 1 is fetched into
+  // stage pa (activations during blocks 0 and 1, weights during block 2), and
+  // block 3 already prepares block 0 of k-tile kt + 1 (stage pn), so no step
+  // starts with dequantisation work that no MFMA overlaps.
   auto step = [&](int p, int kt) {
-    const int pa = (p + NS - 1) % NS;
-    load_x(pa, kt + NS - 1);
-    __builtin_amdgcn_sched_barrier(0);  // the wait counts rely on this issue order
-    load_w(st[pa], min(kt + NS - 1, KT - 1));
+    const int pa = (p + NS - 1) % NS, pn = (p + 1) % NS;
+    const int ka = kt + NS - 1;
+    load_x(pa, ka, 0, MTL / 2);
     __builtin_amdgcn_sched_barrier(0);
-    compute(st[p], xbuf(p));
+    fetch(1, st[p], xbuf(p), 1);
+    mma(0);
+    load_x(pa, ka, MTL / 2, MTL);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(0, st[p], xbuf(p), 2);
+    mma(1);
+    load_w(st[pa], min(ka, KT - 1));  // the wait counts rely on this issue order
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(1, st[p], xbuf(p), 3);
+    mma(0);
     sync_step();
+    make_zs(st[pn]);
+    fetch(0, st[pn], xbuf(pn), 0);
+    mma(1);
   };
 
+  // Prologue: k-tiles 0 .. NS - 2 in flight, block 0 of k-tile 0 prepared.
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p) {
-    load_x(p, p);
+    load_x(p, p, 0, MTL);
     __builtin_amdgcn_sched_barrier(0);
     load_w(st[p], min(p, KT - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
   sync_step();
+  make_zs(st[0]);
+  fetch(0, st[0], xbuf(0), 0);
 
   // Whole rounds of NS k-tiles, then the remaining k-tiles.  A counted loop
   // keeps every step's loads unconditional, so the compiler's wait counts
@@ -271,7 +297,7 @@ template <int BM, typename DT>
 hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
   const dim3 grid((unsigned)(a.gx * a.gy)), block(256);
   switch (gpt) {
-    case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, 3, DT>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, 4, DT>), grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL((tiled_kernel<BM, 2, 3, DT>), grid, block, 0, s, a); break;
     case 4: hipLaunchKernelGGL((tiled_kernel<BM, 4, 2, DT>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
