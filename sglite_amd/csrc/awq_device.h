@@ -192,6 +192,17 @@ __device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Split-K handoff between workgroups (possibly on different XCDs, whose L2s
+// are not coherent with each other) uses device-scope atomics only: partials
+// are written with returning atomic exchanges (complete at the device
+// coherence point before the value returns), the arrival counter is a
+// device-scope fetch-add, and the last workgroup reads the partials back with
+// atomic exchanges.  No agent-scope fence -- i.e. no L2 writeback/invalidate
+// -- is executed.
+__device__ __forceinline__ float xchg_agent(float* p, float v) {
+  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ uint32_t zero_nibble(uint64_t zw, int c) {
   return (uint32_t)(zw >> (4 * c)) & 0xFu;
 }

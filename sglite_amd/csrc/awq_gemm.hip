@@ -100,10 +100,22 @@ bool plan_gemv(const Geom& g, GemmPlan& p) {
   }
 }
 
+// Batches of 17..32 rows on large weight matrices (>= 10 MB of int4) run
+// faster on the tiled kernel with split K than on the decode kernel (graph
+// replay of the Qwen3-4B and Llama-3-8B linears at M = 16, 24, 32 on MI355X:
+// e.g. 26.8 -> 18.6 us for a 2560 x 19456 gate_up at M = 32); smaller
+// matrices stay on the decode kernel.
+bool tiled_preferred(const Geom& g) {
+  const int forced = env_int("SGL_AWQ_TILED_MIN_M", 0);
+  if (forced > 0) return g.M >= forced;
+  return g.M > 32 || (g.M > 16 && g.K * g.N >= 20000000);
+}
+
 GemmPlan plan_gemm(const Geom& g) {
   GemmPlan p{};
-  if (g.M <= 32 && gemv_preferred(g) && plan_gemv(g, p)) return p;
-  if (g.M <= 32) {
+  const bool tiled = tiled_preferred(g);
+  if (!tiled && gemv_preferred(g) && plan_gemv(g, p)) return p;
+  if (!tiled) {
     p.kind = 0;
     // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all
     // variants over the Qwen3-4B and Llama-3-8B decode shapes on MI355X:
@@ -150,16 +162,41 @@ GemmPlan plan_gemm(const Geom& g) {
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
   } else {
     p.kind = 1;
-    int bm = g.M <= 64 ? 64 : 128;
-    const int env = env_int("SGL_AWQ_TILED_BM", 0);
-    if (env == 64 || env == 128) bm = env;
-    if (g.K > tiled_max_k(bm)) bm = 64;
-    p.variant = bm;
+    // Row block and k-slices from a cost model fitted to a sweep over the
+    // Llama-3-8B and Qwen3-4B linears at M = 64 .. 2048 on MI355X (it picks
+    // the measured best, or within 6%, in all 48 cases): time ~ waves of
+    // 256 workgroups x (k-tiles per slice + 1), a 64-row step costing 0.75 of
+    // a 128-row one, plus the partial traffic of the split-K reduction.
+    const int env_bm = env_int("SGL_AWQ_TILED_BM", 0);
+    const int env_ks = env_int("SGL_AWQ_TILED_KS", 0);
+    const int64_t Np = g.NT * 16;
+    double best = 0.0;
+    int best_bm = 0, best_ks = 1;
+    for (int bm : {64, 128}) {
+      if (g.K > tiled_max_k(bm) || ((env_bm == 64 || env_bm == 128) && bm != env_bm)) continue;
+      const int64_t tiles = ((g.NT + 15) / 16) * ((g.M + bm - 1) / bm);
+      for (int ks : {1, 2, 3, 4, 6, 8, 12, 16}) {
+        if (env_ks > 0 ? ks != 1 : (ks > 1 && ks > g.KT / 4)) continue;
+        const int64_t ktc = (g.KT + ks - 1) / ks, kse = (g.KT + ktc - 1) / ktc;
+        const int64_t waves = (tiles * kse + kNumCU - 1) / kNumCU;
+        double t = (double)waves * (double)(ktc + 1) * (bm == 64 ? 0.75 : 1.0);
+        if (kse > 1) t += (double)kse * (double)g.M * (double)Np * 4.0 / 3.2e6;
+        if (best_bm == 0 || t < best) {
+          best = t;
+          best_bm = bm;
+          best_ks = ks;
+        }
+      }
+    }
+    if (best_bm == 0) best_bm = 64;  // K beyond both limits is rejected by the C ABI
+    int64_t ks = env_ks > 0 ? env_ks : best_ks;
+    ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
+    p.variant = best_bm;
     p.grid_x = (g.NT + 15) / 16;
-    p.grid_y = (g.M + bm - 1) / bm;
-    p.ks = 1;
-    p.ktc = (int)g.KT;
-    p.ws_bytes = 0;
+    p.grid_y = (g.M + best_bm - 1) / best_bm;
+    p.ktc = (int)((g.KT + ks - 1) / ks);
+    p.ks = (int)((g.KT + p.ktc - 1) / p.ktc);  // every slice gets >= 1 k-tile
+    p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
   }
   return p;
 }
@@ -169,7 +206,7 @@ hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const vo
                        hipStream_t s) {
   if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
   if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
-  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, s);
+  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
 }
 
 }  // namespace sgl_awq

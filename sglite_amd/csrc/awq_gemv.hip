@@ -35,10 +35,6 @@ namespace sgl_awq {
 
 namespace {
 
-__device__ __forceinline__ float xchg_agent(float* p, float v) {
-  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int NTW, int WN, int WK, int KPW, int MT, int XPT, typename DT>
 __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,

@@ -25,10 +25,10 @@ hipError_t launch_dequant_repacked(const void* w, const void* sr, const void* zr
 
 // GEMM plan: which kernel and how K is split.
 struct GemmPlan {
-  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM, 2 = GEMV (M <= 16)
+  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM, 2 = GEMV (M <= 32)
   int variant;   // kernel template selector
-  int ks;        // k-splits across workgroups (skinny, GEMV)
-  int ktc;       // k-tiles per workgroup (skinny, GEMV)
+  int ks;        // k-splits across workgroups
+  int ktc;       // k-tiles per workgroup
   int xpt;       // activation chunks per thread (GEMV)
   int64_t grid_x, grid_y;
   int64_t ws_bytes;
@@ -45,7 +45,8 @@ hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const vo
                        hipStream_t s);
 int64_t tiled_max_k(int bm);
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, hipStream_t s);
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                        hipStream_t s);
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                        hipStream_t s);

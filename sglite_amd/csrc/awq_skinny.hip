@@ -37,18 +37,10 @@ namespace {
 // for the lane's own column and group slot, and whose B operand holds S of
 // that slot.  So per weight pair the kernel executes a single VALU op.
 //
-// Split-K handoff between workgroups (possibly on different XCDs, whose L2s
-// are not coherent with each other) uses device-scope atomics only: partials
-// are written with returning atomic exchanges (complete at the device
-// coherence point before the value returns), the arrival counter is a
-// device-scope fetch-add, and the last workgroup reads the partials back with
-// atomic exchanges.  No agent-scope fence -- i.e. no L2 writeback/invalidate
-// -- is executed.  The reduction order is fixed (ks = 0, 1, ...), so results
-// are deterministic.
+// Split-K handoff between workgroups: atomic exchanges and a device-scope
+// arrival counter (xchg_agent, awq_device.h).  The reduction order is fixed
+// (ks = 0, 1, ...), so results are deterministic.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float xchg_agent(float* p, float v) {
-  return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 template <int MT, int NTW, int WN, int WK, int GPT, typename DT>
 __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(

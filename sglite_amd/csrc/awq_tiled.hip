@@ -25,6 +25,10 @@
 //   * each k-tile's four 32-row blocks are software-pipelined: block w's MFMAs
 //     run while block w + 1 is dequantised into the other operand buffer.
 //
+// Grids of fewer output tiles than CUs split K: each workgroup computes one
+// k-slice of its tile into an fp32 partial, and a second kernel sums the
+// slices in slice order (deterministic) and stores the output.
+//
 // Workgroups are numbered XCD-aware: the hardware deals consecutive
 // workgroup ids round-robin over the 8 XCDs, and the id -> tile map makes the
 // workgroups that one XCD runs together cover a compact patch of 4 row blocks
@@ -66,8 +70,10 @@ struct TiledArgs {
   const uint64_t* z;
   const void* bias;
   void* out;
+  float* part;  // split-K partials [ks][M][NT * 16]
   int M, N, K, NT, KT, NG, gshift;
   int gx, gy;  // column blocks (256 columns), row blocks (BM rows)
+  int ks, ktc;  // k-slices and k-tiles per slice
 };
 
 // Workgroup id -> (column block, row block).  Ids b, b + 8, b + 16, ... run
@@ -118,8 +124,14 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int c = lane & 15, lg = lane >> 4;
+  // Workgroup -> (output tile, k-slice); k-slices of a tile are launched
+  // tiles apart.
+  const int tiles = a.gx * a.gy;
+  const int kslice = (int)blockIdx.x / tiles;
   int bx, by;
-  tile_of(blockIdx.x, a.gx, a.gy, bx, by);
+  tile_of((int)blockIdx.x - kslice * tiles, a.gx, a.gy, bx, by);
+  const int kt0 = kslice * a.ktc;
+  const int nsteps = min(a.KT - kt0, a.ktc);
   const int m0 = by * BM;
   const int rows = min(BM, a.M - m0);
   const int K = a.K, KT = a.KT, NG = a.NG;
@@ -256,9 +268,9 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // Prologue: k-tiles 0 .. NS - 2 in flight, block 0 of k-tile 0 prepared.
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p) {
-    load_x(p, p, 0, MTL);
+    load_x(p, kt0 + p, 0, MTL);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(st[p], min(p, KT - 1));
+    load_w(st[p], min(kt0 + p, KT - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
   sync_step();
@@ -268,14 +280,15 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // Whole rounds of NS k-tiles, then the remaining k-tiles.  A counted loop
   // keeps every step's loads unconditional, so the compiler's wait counts
   // see the true prefetch distance.
-  int kt = 0;
-  for (; kt + NS <= KT; kt += NS) {
+  // (Prefetches past the k-slice load k-tiles that are never computed.)
+  int i = 0;
+  for (; i + NS <= nsteps; i += NS) {
 #pragma unroll
-    for (int p = 0; p < NS; ++p) step(p, kt + p);
+    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p);
   }
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p)
-    if (kt + p < KT) step(p, kt + p);
+    if (i + p < nsteps) step(p, kt0 + i + p);
 
   // The last steps prefetched past the end; no load may still be writing
   // this workgroup's LDS when it exits.
@@ -283,19 +296,49 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 
   const E* bias = (const E*)a.bias;
   E* out = (E*)a.out;
+  if (a.ks == 1) {
+#pragma unroll
+    for (int mt = 0; mt < MTL; ++mt)
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        const int m = mt * 16 + c;
+        const int n0 = (nt0 + j) * 16 + 4 * lg;
+        if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, acc[mt][j]);
+      }
+    return;
+  }
+
+  // Split K: this slice's partial tile, in fp32, for the reduction kernel.
+  const int64_t Np = (int64_t)a.NT * 16;
 #pragma unroll
   for (int mt = 0; mt < MTL; ++mt)
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       const int m = mt * 16 + c;
       const int n0 = (nt0 + j) * 16 + 4 * lg;
-      if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, acc[mt][j]);
+      if (m < rows && n0 < Np) *(f32x4*)(a.part + ((int64_t)kslice * a.M + m0 + m) * Np + n0) = acc[mt][j];
     }
+}
+
+// Sum of the k-slices' partials in slice order (deterministic), plus bias, in
+// the output dtype.  One thread per four output columns.
+template <typename DT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                            const typename DT::elem* __restrict__ bias,
+                                                            typename DT::elem* __restrict__ out, int M, int N,
+                                                            int Np, int ks) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t m = q / (N / 4);
+  const int64_t n0 = 4 * (q - m * (N / 4));
+  if (m >= M) return;
+  f32x4 sum = *(const f32x4*)(part + m * Np + n0);
+  for (int k = 1; k < ks; ++k) sum += *(const f32x4*)(part + ((int64_t)k * M + m) * Np + n0);
+  store4<DT>(out, bias, m, N, n0, sum);
 }
 
 template <int BM, typename DT>
 hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
-  const dim3 grid((unsigned)(a.gx * a.gy)), block(256);
+  const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);
   switch (gpt) {
     case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, 4, DT>), grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL((tiled_kernel<BM, 2, 3, DT>), grid, block, 0, s, a); break;
@@ -321,8 +364,9 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
 int64_t tiled_max_k(int bm) { return ((int64_t(1) << 31) - 1) / (2 * (int64_t)bm); }
 
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, hipStream_t s) {
-  if (p.grid_x * p.grid_y >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                        hipStream_t s) {
+  if (p.grid_x * p.grid_y * p.ks >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
   TiledArgs a;
   a.x = x;
   a.w = (const u32x4*)w;
@@ -339,9 +383,22 @@ hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const v
   a.gshift = g.gshift;
   a.gx = (int)p.grid_x;
   a.gy = (int)p.grid_y;
+  a.ks = p.ks;
+  a.ktc = p.ktc;
+  a.part = (float*)ws;
   // Groups per 128-row k-tile: 1 for G >= 128 (or one group), else 128 / G.
   const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
-  return dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
+  hipError_t e = dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
+  if (e != hipSuccess || p.ks == 1) return e;
+  const int64_t quads = g.M * (g.N / 4);
+  const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
+  if (dtype == 0)
+    hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, block, 0, s, (const float*)ws, (const _Float16*)bias,
+                       (_Float16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, block, 0, s, (const float*)ws, (const __bf16*)bias,
+                       (__bf16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks);
+  return hipGetLastError();
 }
 
 }  // namespace sgl_awq

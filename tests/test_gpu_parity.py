@@ -376,18 +376,43 @@ def test_every_tiled_variant(bm, G, dtype, monkeypatch):
     """Each prefill-kernel instantiation (row block x groups per 128-row
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
-    leave the last row block partial; pipelines of 2 and 3 stages, whole
-    rounds plus a remainder."""
+    leave the last row block partial; whole pipeline rounds plus a
+    remainder, with and without split K."""
     ops = _ops()
     K = {32: 2336, 64: 2368, 128: 2432, -1: 1120}[G]
     N = 264
     t, d = _linear(K, N, G, seed=bm + (G if G > 0 else 5), dtype=dtype)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
     monkeypatch.setenv("SGL_AWQ_TILED_BM", str(bm))
-    for M in (33, 130, 257):
-        x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
-        y = ops.gemm(x.to(DEV), r, K, N, G)
-        ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
-        ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
-        assert ok, (bm, G, M, err, mx)
+    for ks in (1, 3):  # whole K per workgroup, and three k-slices
+        monkeypatch.setenv("SGL_AWQ_TILED_KS", str(ks))
+        for M in (33, 130, 257):
+            x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
+            y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
+            ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+            ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+            assert ok, (bm, G, ks, M, err, mx)
+    assert int(cnt.abs().sum()) == 0
     assert ops.gemm_kernel(130, N, K, G) == "tiled_kernel"
+
+
+@pytest.mark.parametrize("M,K,N,G", [(64, 14336, 4096, 128), (200, 4096, 2560, 64), (40, 2368, 264, 32)])
+def test_tiled_split_k_parity_and_determinism(M, K, N, G):
+    """Prefill-kernel grids with fewer output tiles than CUs split K across
+    workgroups; the last slice reduces in slice order, so repeated calls are
+    bit-identical, and the arrival counters are left at zero."""
+    ops = _ops()
+    assert ops.gemm_kernel(M, N, K, G) == "tiled_kernel"
+    assert ops.workspace_bytes(M, N, K, G) > 0
+    t, d = _linear(K, N, G, seed=M + K)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    x = oracle.make_activation(M, K, seed=M)
+    ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+    ys = [ops.gemm(x.to(DEV), r, K, N, G, counters=cnt) for _ in range(3)]
+    ok, err, mx = oracle.tolerance_ok(ys[0], ref, TOL)
+    assert ok, (err, mx)
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    assert int(cnt.abs().sum()) == 0

@@ -68,7 +68,14 @@ def test_workspace_query_is_bounded():
             assert ws % (4 * M * 16) == 0
             # split-K partials stay well below the int4 weight stream
             assert ws <= K * N // 2
-        assert lib.awq_workspace_bytes(2048, N, K, 128) == 0  # tiled kernel needs no scratch
+        # prefill kernel: scratch only when it splits K (small grids), then
+        # ks slices of fp32 partials, 2 <= ks <= 16
+        NT = (N + 15) // 16
+        for M in (64, 512, 2048):
+            ws = lib.awq_workspace_bytes(M, N, K, 128)
+            ks, rem = divmod(ws, M * NT * 16 * 4)
+            assert rem == 0 and (ks == 0 or 2 <= ks <= 16)
+    assert lib.awq_workspace_bytes(8192, 28672, 4096, 128) == 0  # full grids never split
 
 
 @pytest.mark.parametrize("K,N,G,dtype,msg", [
