@@ -30,6 +30,14 @@ Also reported on the same line:
                 cores for one pass of the layer at M = 1, 8, 32.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Profiles (summaries committed under profiles/):
+  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --steps 500 \
+      --no-cpu-baseline --no-prefill --no-moe;  python3 bench.py --rocprof-summary decode <dir>
+  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --no-decode \
+      --no-moe --no-cpu-baseline;  python3 bench.py --rocprof-summary prefill <dir>
+  rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) ... -- python3 bench.py --pmc-workload;
+      python3 bench.py --pmc-summary <fetch_dir> <write_dir>
 """
 
 from __future__ import annotations
@@ -52,6 +60,7 @@ G = 128
 LAYER = [("qkv_proj", 2560, 6144), ("o_proj", 4096, 2560), ("gate_up_proj", 2560, 19456), ("down_proj", 9728, 2560)]
 PREFILL = [("qkv_proj", 4096, 6144), ("o_proj", 4096, 4096), ("gate_up_proj", 4096, 28672), ("down_proj", 14336, 4096)]
 M_SET = (1, 8, 32)
+PREFILL_M = 2048
 AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
 
 
@@ -319,124 +328,107 @@ def committed_traffic(kernel: str):
     return None
 
 
-def rocprof_summary(trace_dir: str, command: str) -> str:
-    """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
+DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel")
+TRACE_KERNELS = DECODE_KERNELS + ("splitk_reduce_kernel", "moe_")
 
-    The decode phase launches every (M, linear) of the layer equally often,
-    so the mean algorithmic bytes per decode launch is step_bytes / 12 and
-    the roofline figure is that over the mean skinny_kernel duration.
-    """
+
+def _trace_groups(trace_dir: str):
+    """Kernel-trace durations (us) grouped by (short name, grid, block)."""
     import csv
     import glob
     from collections import defaultdict
 
     path = sorted(glob.glob(os.path.join(trace_dir, "*kernel_trace.csv")))[0]
-    rows = list(csv.DictReader(open(path)))
     groups = defaultdict(list)
-    for r in rows:
+    for r in csv.DictReader(open(path)):
         name = r["Kernel_Name"]
-        if not any(k in name for k in ("skinny_kernel", "tiled_kernel", "gemv_kernel")):
+        if not any(k in name for k in TRACE_KERNELS):
             continue
         short = name.replace("(anonymous namespace)::", "").replace("sgl_awq::", "").replace("void ", "")
         short = short[:short.index("(")] if "(" in short else short
-        key = (short, r["Grid_Size_X"], r["Grid_Size_Y"], r["Workgroup_Size_X"])
+        bx = int(r["Workgroup_Size_X"])
+        key = (short, int(r["Grid_Size_X"]) // bx, int(r["Grid_Size_Y"]), bx)
         groups[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return groups
+
+
+def _trace_table(groups) -> list:
+    lines = ["| kernel | grid (x, y) | block | dispatches | mean us | min us | max us |",
+             "|---|---|---|---|---|---|---|"]
+    for (name, gx, gy, bx), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{name}` | {gx}, {gy} | {bx} | {len(ds)} | {sum(ds) / len(ds):.2f} | "
+                     f"{min(ds):.2f} | {max(ds):.2f} |")
+    return lines
+
+
+def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
+    """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
+
+    decode: every (M, linear) of the step is launched equally often, so a
+    kernel's mean algorithmic bytes per launch is the mean over the (M, linear)
+    pairs it serves (ops.gemm_kernel names the kernel of each shape); a split-K
+    GEMM on the tiled kernel also runs splitk_reduce_kernel, listed apart.
+    prefill: the four linears at M = 2048 are each launched 13 times (3
+    warm-up + 10 timed); TFLOP/s = their FLOPs over the summed durations of the
+    tiled (and reduce) kernels.
+    """
     from sglite_amd import ops
 
-    lines = [
-        "# Decode kernels on the Qwen3-4B layer workload (M = 1, 8, 32), rocprofv3 kernel trace",
-        "",
-        f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
-        "",
-        "Every (M, linear) of the step is launched equally often, so a kernel's mean algorithmic bytes per",
-        "launch is the mean over the (M, linear) pairs it serves.",
-        "",
-    ]
-    for kern in ("skinny_kernel", "gemv_kernel"):
-        pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.gemm_kernel(M, N, K, G) == kern]
-        ds = [d for (k, *_), v in groups.items() if k.startswith(kern.split("_")[0]) for d in v]
-        if not pairs or not ds:
-            continue
-        mean_b = sum(gemm_bytes(*p) for p in pairs) / len(pairs)
-        mean_us = sum(ds) / len(ds)
-        lines.append(f"* `{kern}`: {len(pairs)} of the step's {len(M_SET) * len(LAYER)} launches; "
-                     f"{len(ds)} dispatches, mean duration {mean_us:.3f} us; mean algorithmic bytes "
-                     f"{mean_b / 1e6:.3f} MB; achieved {mean_b / mean_us / 1e3:.1f} GB/s = "
-                     f"{mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.")
-    lines += [
-        "",
-        "| kernel | grid (x, y) | block | dispatches | mean us | min us | max us |",
-        "|---|---|---|---|---|---|---|",
-    ]
-    for (name, gx, gy, bx), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"| `{name}` | {int(gx) // int(bx)}, {gy} | {bx} | {len(ds)} | {sum(ds) / len(ds):.2f} | "
-                     f"{min(ds):.2f} | {max(ds):.2f} |")
+    groups = _trace_groups(trace_dir)
+    if section == "decode":
+        lines = [
+            "# Decode kernels on the Qwen3-4B layer workload (M = 1, 8, 32), rocprofv3 kernel trace",
+            "",
+            f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
+            "",
+            "Every (M, linear) of the step is launched equally often, so a kernel's mean algorithmic bytes per",
+            "launch is the mean over the (M, linear) pairs it serves.  Split-K GEMMs on the tiled kernel also",
+            "launch `splitk_reduce_kernel` (listed in the table, not in the kernel's duration).",
+            "",
+        ]
+        for kern in DECODE_KERNELS:
+            pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.gemm_kernel(M, N, K, G) == kern]
+            ds = [d for (k, *_), v in groups.items() if k.startswith(kern + "<") for d in v]
+            if not pairs or not ds:
+                continue
+            mean_b = sum(gemm_bytes(*p) for p in pairs) / len(pairs)
+            mean_us = sum(ds) / len(ds)
+            lines.append(f"* `{kern}`: {len(pairs)} of the step's {len(M_SET) * len(LAYER)} launches; "
+                         f"{len(ds)} dispatches, mean duration {mean_us:.3f} us; mean algorithmic bytes "
+                         f"{mean_b / 1e6:.3f} MB; achieved {mean_b / mean_us / 1e3:.1f} GB/s = "
+                         f"{mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.")
+    else:
+        M = PREFILL_M
+        flops = 13 * sum(2 * M * N * K for _, K, N in PREFILL)
+        us = sum(d for (k, *_), v in groups.items() if k.startswith(("tiled_kernel<", "splitk_reduce_kernel<"))
+                 for d in v)
+        tf = flops / us / 1e6
+        lines = [
+            f"# Prefill kernel on the Llama-3-8B linears at M = {M}, rocprofv3 kernel trace",
+            "",
+            f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
+            "",
+            "Each linear (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, down 14336x4096) is launched 13 times",
+            "(3 warm-up + 10 timed), fp16, int4 group 128.",
+            "",
+            f"* `tiled_kernel`: {sum(len(v) for (k, *_), v in groups.items() if k.startswith('tiled_kernel<'))} "
+            f"dispatches, {us:.1f} us in total for {flops / 1e12:.3f} TFLOP: {tf:.1f} TFLOP/s = "
+            f"{tf / MFMA_FP16_PEAK_TFLOPS:.4f} of 2.5 PFLOP/s dense fp16 MFMA.",
+        ]
+    lines += [""] + _trace_table(groups)
     return "\n".join(lines) + "\n"
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--copies", type=int, default=36, help="distinct weight copies rotated through")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--no-moe", action="store_true")
-    ap.add_argument("--rocprof-summary", metavar="TRACE_DIR",
-                    help="print a markdown summary of a rocprofv3 --kernel-trace run of this script and exit")
-    ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
-                                                  "python3 bench.py --steps 500 --no-cpu-baseline")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
-    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="print a markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --pmc-workload")
-    args = ap.parse_args()
-    if args.rocprof_summary:
-        print(rocprof_summary(args.rocprof_summary, args.rocprof_command), end="")
-        return 0
-    if args.pmc_summary:
-        print(pmc_summary(*args.pmc_summary), end="")
-        return 0
-    if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
-              "design, not a measured path", file=sys.stderr)
-        return 2
-    if not torch.cuda.is_available():
-        print("bench.py needs an MI355X", file=sys.stderr)
-        return 2
-
-    from sglite_amd import ops
-
-    dev = torch.device("cuda:0")
-    gen = torch.Generator(device=dev).manual_seed(0)
-    if args.pmc_workload:
-        return pmc_workload(ops, dev, gen)
-    C = args.copies
-    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in LAYER} for _ in range(C)]
-    cnts = [{name: ops.make_counters(N, dev) for name, K, N in LAYER} for _ in range(C)]
-    xg = torch.Generator(device=dev).manual_seed(1)
-    xs = {(M, K): torch.randn((M, K), generator=xg, device=dev).to(torch.float16)
-          for M in M_SET for K in {k for _, k, _ in LAYER}}
-    outs = {(M, name): torch.empty((M, N), dtype=torch.float16, device=dev) for M in M_SET for name, _, N in LAYER}
-    torch.cuda.synchronize()
-
-    def linear(c, M, name, K, N):
-        ops.gemm(xs[(M, K)], reps[c][name], K, N, G, counters=cnts[c][name], out=outs[(M, name)])
-
-    def step_fn(c):
-        def f():
-            for M in M_SET:
-                for name, K, N in LAYER:
-                    linear(c, M, name, K, N)
-        return f
-
+def decode_bench(ops, args, C, linear, step_fn, step_bytes):
+    """The decode step: graph replays over the C weight copies, then
+    per-launch durations of every (M, linear) and the dominant kernel's
+    roofline figures."""
     steps = [graph_of(step_fn(c)) for c in range(C)]
-    step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
     time_replays(steps, args.warmup)
     ms = time_replays(steps, args.steps)
     ms_per_step = ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del steps
 
     # Per-launch durations of the decode kernel: graphs of C back-to-back
     # launches of one (M, linear) over the C weight copies.
@@ -472,12 +464,83 @@ def main() -> int:
                 "us_per_launch_avg": round(d["us"] / d["launches"], 3)}
     kernels = {k: {"launches_per_step": v["launches"], "GB/s": round(v["bytes"] / v["us"] / 1e3, 1),
                    "us_per_step": round(v["us"], 3)} for k, v in per_kernel.items()}
-    del steps
+    return value, ms_per_step, roofline, kernels, per_m
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--copies", type=int, default=36, help="distinct weight copies rotated through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the decode step (profiling runs of the other sections; no value is reported)")
+    ap.add_argument("--rocprof-summary", nargs=2, metavar=("SECTION", "TRACE_DIR"),
+                    help="print a markdown summary (decode or prefill) of a rocprofv3 --kernel-trace run "
+                         "of this script and exit")
+    ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
+                                                  "python3 bench.py <args>",
+                    help="the profiled command, quoted in the summary's header")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print a markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --pmc-workload")
+    args = ap.parse_args()
+    if args.rocprof_summary:
+        section, trace_dir = args.rocprof_summary
+        print(rocprof_summary(trace_dir, args.rocprof_command, section), end="")
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary), end="")
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
+              "design, not a measured path", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X", file=sys.stderr)
+        return 2
+
+    from sglite_amd import ops
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    if args.pmc_workload:
+        return pmc_workload(ops, dev, gen)
+    C = args.copies
+    if args.no_decode:
+        C = 0
+    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in LAYER} for _ in range(C)]
+    cnts = [{name: ops.make_counters(N, dev) for name, K, N in LAYER} for _ in range(C)]
+    xg = torch.Generator(device=dev).manual_seed(1)
+    xs = {(M, K): torch.randn((M, K), generator=xg, device=dev).to(torch.float16)
+          for M in M_SET for K in {k for _, k, _ in LAYER}}
+    outs = {(M, name): torch.empty((M, N), dtype=torch.float16, device=dev) for M in M_SET for name, _, N in LAYER}
+    torch.cuda.synchronize()
+
+    def linear(c, M, name, K, N):
+        ops.gemm(xs[(M, K)], reps[c][name], K, N, G, counters=cnts[c][name], out=outs[(M, name)])
+
+    def step_fn(c):
+        def f():
+            for M in M_SET:
+                for name, K, N in LAYER:
+                    linear(c, M, name, K, N)
+        return f
+
+    step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
+    value, ms_per_step, roofline, kernels, per_m = None, None, None, None, None
+    if C > 0:
+        value, ms_per_step, roofline, kernels, per_m = decode_bench(ops, args, C, linear, step_fn, step_bytes)
+
     torch.cuda.synchronize()
 
     prefill = None
     if not args.no_prefill:
-        M = 2048
+        M = PREFILL_M
         x = {K: torch.randn((M, K), generator=xg, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
         tot_f, tot_t, lin = 0, 0.0, {}
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -512,12 +575,12 @@ def main() -> int:
 
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": None if value is None else round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": None if ms_per_step is None else round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
