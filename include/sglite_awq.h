@@ -17,6 +17,8 @@
  * G is the group size: 32, 64, 128 or K (-1 is accepted and means K).
  * Requirements: K % 32 == 0, K % G == 0, N % 8 == 0 (the AWQ linear method's
  * own checks, python/sglite/srt/model_executor/layers/quantization/awq.py:76-85).
+ * Engine limits (AWQ_STATUS_UNSUPPORTED beyond them): K < 2^24, N < 2^30,
+ * M < 2^24 (the kernels address one workgroup's rows with 32-bit offsets).
  */
 #ifndef SGLITE_AWQ_H
 #define SGLITE_AWQ_H
