@@ -100,15 +100,19 @@ bool plan_gemv(const Geom& g, GemmPlan& p) {
   }
 }
 
-// Batches of 17..32 rows on large weight matrices (>= 10 MB of int4) run
-// faster on the tiled kernel with split K than on the decode kernel (graph
-// replay of the Qwen3-4B and Llama-3-8B linears at M = 16, 24, 32 on MI355X:
-// e.g. 26.8 -> 18.6 us for a 2560 x 19456 gate_up at M = 32); smaller
-// matrices stay on the decode kernel.
+// Batches of 16..32 rows: the tiled kernel (32-row block, split K) beats the
+// decode kernel on wide or deep matrices (graph replay of the Qwen3-4B and
+// Llama-3-8B linears at M = 16, 24, 32 on MI355X: at M = 32 qkv, gate_up and
+// down run 8-15% faster, e.g. 29.1 -> 24.7 us for a 4096 x 28672 gate_up;
+// the o_proj shapes stay 8-15% faster on the decode kernel); at M = 16 only
+// gate_up-sized matrices gain.
 bool tiled_preferred(const Geom& g) {
   const int forced = env_int("SGL_AWQ_TILED_MIN_M", 0);
   if (forced > 0) return g.M >= forced;
-  return g.M > 32 || (g.M > 16 && g.K * g.N >= 20000000);
+  if (g.M > 32) return true;
+  const int64_t kn = g.K * g.N;
+  if (g.M > 16) return kn >= 12000000 && (g.N >= 6144 || g.K >= 8192);
+  return g.M == 16 && g.N >= 16384 && kn >= 20000000;
 }
 
 GemmPlan plan_gemm(const Geom& g) {
@@ -162,24 +166,27 @@ GemmPlan plan_gemm(const Geom& g) {
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
   } else {
     p.kind = 1;
-    // Row block and k-slices from a cost model fitted to a sweep over the
-    // Llama-3-8B and Qwen3-4B linears at M = 64 .. 2048 on MI355X (it picks
-    // the measured best, or within 6%, in all 48 cases): time ~ waves of
-    // 256 workgroups x (k-tiles per slice + 1), a 64-row step costing 0.75 of
-    // a 128-row one, plus the partial traffic of the split-K reduction.
+    // Row block and k-slices from a cost model fitted to sweeps over the
+    // Llama-3-8B and Qwen3-4B linears at M = 16 .. 2048 on MI355X (it picks
+    // the measured best, or within 6%, in 71 of 72 cases): time ~ waves of
+    // 256 workgroups x (k-tiles per slice + 1), a 64-row step costing 0.75
+    // and a 32-row step 0.3 of a 128-row one, plus the partial traffic of the
+    // split-K reduction.  The 32-row block serves batches of at most 32 rows.
     const int env_bm = env_int("SGL_AWQ_TILED_BM", 0);
+    const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128;
     const int env_ks = env_int("SGL_AWQ_TILED_KS", 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int bm : {64, 128}) {
-      if (g.K > tiled_max_k(bm) || ((env_bm == 64 || env_bm == 128) && bm != env_bm)) continue;
+    for (int bm : {32, 64, 128}) {
+      if (g.K > tiled_max_k(bm) || (env_bm_ok && bm != env_bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
       const int64_t tiles = ((g.NT + 15) / 16) * ((g.M + bm - 1) / bm);
+      const int64_t min_ktc = g.M <= 32 ? 2 : 4;  // k-tiles per slice at least
       for (int ks : {1, 2, 3, 4, 6, 8, 12, 16}) {
-        if (env_ks > 0 ? ks != 1 : (ks > 1 && ks > g.KT / 4)) continue;
+        if (env_ks > 0 ? ks != 1 : (ks > 1 && ks > g.KT / min_ktc)) continue;
         const int64_t ktc = (g.KT + ks - 1) / ks, kse = (g.KT + ktc - 1) / ktc;
         const int64_t waves = (tiles * kse + kNumCU - 1) / kNumCU;
-        double t = (double)waves * (double)(ktc + 1) * (bm == 64 ? 0.75 : 1.0);
+        double t = (double)waves * (double)(ktc + 1) * (bm == 32 ? 0.3 : (bm == 64 ? 0.75 : 1.0));
         if (kse > 1) t += (double)kse * (double)g.M * (double)Np * 4.0 / 3.2e6;
         if (best_bm == 0 || t < best) {
           best = t;
@@ -188,7 +195,7 @@ GemmPlan plan_gemm(const Geom& g) {
         }
       }
     }
-    if (best_bm == 0) best_bm = 64;  // K beyond both limits is rejected by the C ABI
+    if (best_bm == 0) best_bm = 64;  // K beyond every limit is rejected by the C ABI
     int64_t ks = env_ks > 0 ? env_ks : best_ks;
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
     p.variant = best_bm;

@@ -119,7 +119,10 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   __shared__ u32x4 xs1[XS];
   __shared__ u32x4 xs2[NS > 2 ? XS : 1];
   __shared__ u32x4 xs3[NS > 3 ? XS : 1];
-  auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : xs3)); };
+  __shared__ u32x4 xs4[NS > 4 ? XS : 1];
+  auto xbuf = [&](int p) -> u32x4* {
+    return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : (p == 3 ? xs3 : xs4)));
+  };
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -336,11 +339,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   store4<DT>(out, bias, m, N, n0, sum);
 }
 
+// Pipeline depth: 4 stages (3 for G = 64, 2 for G = 32, whose zero/scale
+// loads per stage are 2x / 4x); the 32-row variant, latency-bound, 5.
 template <int BM, typename DT>
 hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
   const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);
+  constexpr int NS1 = BM == 32 ? 5 : 4;
   switch (gpt) {
-    case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, 4, DT>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((tiled_kernel<BM, 1, NS1, DT>), grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL((tiled_kernel<BM, 2, 3, DT>), grid, block, 0, s, a); break;
     case 4: hipLaunchKernelGGL((tiled_kernel<BM, 4, 2, DT>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
@@ -351,6 +357,7 @@ hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
 template <typename DT>
 hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t s) {
   switch (p.variant) {
+    case 32: return launch_bm<32, DT>(a, gpt, s);
     case 64: return launch_bm<64, DT>(a, gpt, s);
     case 128: return launch_bm<128, DT>(a, gpt, s);
     default: return hipErrorInvalidValue;

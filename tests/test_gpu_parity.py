@@ -369,7 +369,7 @@ def test_gemv_bf16_and_bias(M):
     assert ok, (err, mx)
 
 
-@pytest.mark.parametrize("bm", [64, 128])
+@pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_every_tiled_variant(bm, G, dtype, monkeypatch):
@@ -385,16 +385,17 @@ def test_every_tiled_variant(bm, G, dtype, monkeypatch):
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
     monkeypatch.setenv("SGL_AWQ_TILED_BM", str(bm))
+    monkeypatch.setenv("SGL_AWQ_TILED_MIN_M", "1")  # small batches through this kernel too
     for ks in (1, 3):  # whole K per workgroup, and three k-slices
         monkeypatch.setenv("SGL_AWQ_TILED_KS", str(ks))
-        for M in (33, 130, 257):
+        for M in (20, 33, 130, 257):
             x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
             ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
             ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
             assert ok, (bm, G, ks, M, err, mx)
     assert int(cnt.abs().sum()) == 0
-    assert ops.gemm_kernel(130, N, K, G) == "tiled_kernel"
+    assert ops.gemm_kernel(20, N, K, G) == "tiled_kernel"
 
 
 @pytest.mark.parametrize("M,K,N,G", [(64, 14336, 4096, 128), (200, 4096, 2560, 64), (40, 2368, 264, 32)])
