@@ -185,6 +185,7 @@ GemmPlan plan_gemm(const Geom& g) {
       for (int ks : {1, 2, 3, 4, 6, 8, 12, 16}) {
         if (env_ks > 0 ? ks != 1 : (ks > 1 && ks > g.KT / min_ktc)) continue;
         const int64_t ktc = (g.KT + ks - 1) / ks, kse = (g.KT + ktc - 1) / ktc;
+        if (kse > 1 && kse * g.M * Np * 4 >= (int64_t(1) << 31)) continue;  // 32-bit partial offsets
         const int64_t waves = (tiles * kse + kNumCU - 1) / kNumCU;
         double t = (double)waves * (double)(ktc + 1) * (bm == 32 ? 0.3 : (bm == 64 ? 0.75 : 1.0));
         if (kse > 1) t += (double)kse * (double)g.M * (double)Np * 4.0 / 3.2e6;
@@ -198,6 +199,7 @@ GemmPlan plan_gemm(const Geom& g) {
     if (best_bm == 0) best_bm = 64;  // K beyond every limit is rejected by the C ABI
     int64_t ks = env_ks > 0 ? env_ks : best_ks;
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
+    while (ks > 1 && ks * g.M * Np * 4 >= (int64_t(1) << 31)) --ks;
     p.variant = best_bm;
     p.grid_x = (g.NT + 15) / 16;
     p.grid_y = (g.M + best_bm - 1) / best_bm;

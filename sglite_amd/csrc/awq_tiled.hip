@@ -324,7 +324,9 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 }
 
 // Sum of the k-slices' partials in slice order (deterministic), plus bias, in
-// the output dtype.  One thread per four output columns.
+// the output dtype.  One thread per four output columns; the slices are read
+// four at a time, all four loads in flight (slices past ks read as zeros
+// through the buffer range).
 template <typename DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
                                                             const typename DT::elem* __restrict__ bias,
@@ -334,13 +336,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t m = q / (N / 4);
   const int64_t n0 = 4 * (q - m * (N / 4));
   if (m >= M) return;
-  f32x4 sum = *(const f32x4*)(part + m * Np + n0);
-  for (int k = 1; k < ks; ++k) sum += *(const f32x4*)(part + ((int64_t)k * M + m) * Np + n0);
+  const uint32_t slice = (uint32_t)M * (uint32_t)Np * 4u;  // bytes per k-slice
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(part, slice * (uint32_t)ks);
+  const uint32_t off = ((uint32_t)m * (uint32_t)Np + (uint32_t)n0) * 4u;
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < ks; k += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + (uint32_t)i * slice,
+                                                                              (int)((uint32_t)k * slice), 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum += v[i];
+  }
   store4<DT>(out, bias, m, N, n0, sum);
 }
 
-// Pipeline depth: 4 stages (3 for G = 64, 2 for G = 32, whose zero/scale
-// loads per stage are 2x / 4x); the 32-row variant, latency-bound, 5.
 template <int BM, typename DT>
 hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
   const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);

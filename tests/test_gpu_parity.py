@@ -398,11 +398,15 @@ def test_every_tiled_variant(bm, G, dtype, monkeypatch):
     assert ops.gemm_kernel(20, N, K, G) == "tiled_kernel"
 
 
-@pytest.mark.parametrize("M,K,N,G", [(64, 14336, 4096, 128), (200, 4096, 2560, 64), (40, 2368, 264, 32)])
+@pytest.mark.parametrize("M,K,N,G", [(64, 14336, 4096, 128), (200, 4096, 2560, 64), (40, 2368, 264, 32),
+                                     (24, 4096, 28672, 128), (2048, 8192, 264, 128)])
 def test_tiled_split_k_parity_and_determinism(M, K, N, G):
     """Prefill-kernel grids with fewer output tiles than CUs split K across
-    workgroups; the last slice reduces in slice order, so repeated calls are
-    bit-identical, and the arrival counters are left at zero."""
+    workgroups.  The last slice to arrive reduces the tile (or, when the
+    grid has more output tiles than the counter buffer holds -- the last
+    case -- a second kernel does), always in slice order: repeated calls and
+    graph replays are bit-identical, and the arrival counters are left at
+    zero."""
     ops = _ops()
     assert ops.gemm_kernel(M, N, K, G) == "tiled_kernel"
     assert ops.workspace_bytes(M, N, K, G) > 0
@@ -411,9 +415,20 @@ def test_tiled_split_k_parity_and_determinism(M, K, N, G):
     cnt = ops.make_counters(N, DEV)
     x = oracle.make_activation(M, K, seed=M)
     ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
-    ys = [ops.gemm(x.to(DEV), r, K, N, G, counters=cnt) for _ in range(3)]
+    xd = x.to(DEV)
+    ys = [ops.gemm(xd, r, K, N, G, counters=cnt) for _ in range(10)]
     ok, err, mx = oracle.tolerance_ok(ys[0], ref, TOL)
     assert ok, (err, mx)
     for y in ys[1:]:
         assert torch.equal(y, ys[0])
+    assert int(cnt.abs().sum()) == 0
+    out = torch.empty_like(ys[0])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.gemm(xd, r, K, N, G, counters=cnt, out=out)
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ys[0])
     assert int(cnt.abs().sum()) == 0
