@@ -26,6 +26,8 @@ Also reported on the same line:
   per_m         the same per batch size.
   prefill       Llama-3-8B's four linears at M = 2048, TFLOP/s against the
                 2.5 PFLOP/s dense fp16 MFMA peak (MFMA-bound regime).
+  stack70b      the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at M = 64
+                (GB/s) and M = 4096 (TFLOP/s), layer after layer.
   cpu_baseline  the CPU oracle (dequantise + fp32 matmul + cast) on the host
                 cores for one pass of the layer at M = 1, 8, 32.
 
@@ -84,6 +86,66 @@ def make_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device):
     r = ops.repack(pack_awq_gpu(q), pack_awq_gpu(z), s)
     del q, z, s
     return r
+
+
+STACK70B = [("qkv_proj", 8192, 10240), ("o_proj", 8192, 8192), ("gate_up_proj", 8192, 57344),
+            ("down_proj", 28672, 8192)]
+STACK70B_LAYERS = 80
+
+
+def random_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device):
+    """A linear's repacked tensors filled directly with random nibbles, zero
+    points and U[0.002, 0.02] fp16 scales (the CDNA4 layout of random AWQ
+    tensors is random in the same way), without the AWQ round trip."""
+    wb, sb, zb = ops.repacked_sizes(K, N, G)
+    w = torch.randint(-2**31, 2**31, (wb // 4,), generator=gen, device=dev, dtype=torch.int32)
+    z = torch.randint(-2**31, 2**31, (zb // 4,), generator=gen, device=dev, dtype=torch.int32).view(torch.int64)
+    s = (torch.rand((sb // 2,), generator=gen, device=dev) * 0.018 + 0.002).to(torch.float16)
+    NT, NG = (N + 15) // 16, K // G
+    return ops.Repacked(w, s.view(NT, NG, 16), z.view(NT, NG))
+
+
+def stack70b_bench(ops, dev: torch.device, gen: torch.Generator) -> dict:
+    """Llama-3.1-70B-shaped AWQ stack on one GPU: 80 layers x {qkv 8192->10240,
+    o 8192->8192, gate_up 8192->57344, down 28672->8192}, int4 group 128
+    (35.6 GB of int4 weights, zeros and scales), run layer after layer at
+    M = 64 (a batched decode step: whole-stack weight-stream GB/s) and
+    M = 4096 (a prefill chunk: TFLOP/s).  Each linear reads a fixed random
+    activation of its input width (values are not carried from layer to
+    layer: without the model's norms they would overflow); launches are
+    back to back on one stream, as in the model."""
+    layers = [{name: random_repacked(ops, K, N, gen, dev) for name, K, N in STACK70B}
+              for _ in range(STACK70B_LAYERS)]
+    cnts = {name: ops.make_counters(N, dev) for name, K, N in STACK70B}
+    res = {}
+    for M, passes in ((64, 5), (4096, 2)):
+        xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.float16) for _, K, _ in STACK70B}
+        outs = {name: torch.empty((M, N), dtype=torch.float16, device=dev) for name, _, N in STACK70B}
+
+        def stack():
+            for lay in layers:
+                for name, K, N in STACK70B:
+                    ops.gemm(xs[K], lay[name], K, N, G, counters=cnts[name], out=outs[name])
+
+        stack()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(passes):
+            stack()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / passes
+        byt = STACK70B_LAYERS * sum(gemm_bytes(M, N, K) for _, K, N in STACK70B)
+        fl = STACK70B_LAYERS * sum(2 * M * N * K for _, K, N in STACK70B)
+        res[str(M)] = {"ms_per_pass": round(ms, 2), "GB/s": round(byt / ms / 1e6, 1),
+                       "TFLOP/s": round(fl / ms / 1e9, 1)}
+        del xs, outs
+    del layers
+    torch.cuda.synchronize()
+    return {"workload": "Llama-3.1-70B-shaped AWQ stack, 80 x {qkv 8192x10240, o 8192x8192, gate_up 8192x57344, "
+                        "down 28672x8192}, int4 group 128 with zeros, fp16; layer-by-layer launches",
+            "weight_bytes": STACK70B_LAYERS * sum(gemm_bytes(0, N, K) for _, K, N in STACK70B), "per_m": res}
 
 
 def graph_of(fn) -> torch.cuda.CUDAGraph:
@@ -476,6 +538,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 70B-shaped stack (35.6 GB of weights)")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the decode step (profiling runs of the other sections; no value is reported)")
     ap.add_argument("--rocprof-summary", nargs=2, metavar=("SECTION", "TRACE_DIR"),
@@ -570,6 +633,7 @@ def main() -> int:
                    "kernel": "tiled_kernel", "linears": lin}
 
     moe = None if args.no_moe else moe_bench(ops, dev, gen)
+    stack = None if args.no_stack else stack70b_bench(ops, dev, gen)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline()
 
@@ -596,6 +660,7 @@ def main() -> int:
         "per_m": per_m,
         "prefill": prefill,
         "moe": moe,
+        "stack70b": stack,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
