@@ -24,8 +24,12 @@ def create_moe_backend(backend: str) -> BaseMoeBackend:
         raise ValueError(f"unknown MoE backend {backend!r}; registered: {sorted(SUPPORTED_MOE_BACKENDS)}") from None
 
 
+from .layer import AWQExpertStack, AWQMoELayer  # noqa: E402  (the layer resolves backends by name)
+
 __all__ = [
+    "AWQExpertStack",
     "AWQFusedMoe",
+    "AWQMoELayer",
     "AWQMoeWeights",
     "BaseMoeBackend",
     "SUPPORTED_MOE_BACKENDS",
