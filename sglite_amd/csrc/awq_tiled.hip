@@ -47,6 +47,7 @@ namespace sgl_awq {
 namespace {
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
+constexpr int kCacheDevice = 16;              // buffer cache policy: device scope (sc1)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
@@ -135,6 +136,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   tile_of((int)blockIdx.x - kslice * tiles, a.gx, a.gy, bx, by);
   const int kt0 = kslice * a.ktc;
   const int nsteps = min(a.KT - kt0, a.ktc);
+  const int kend = kt0 + nsteps;  // k-tiles from kend on belong to other slices
   const int m0 = by * BM;
   const int rows = min(BM, a.M - m0);
   const int K = a.K, KT = a.KT, NG = a.NG;
@@ -162,6 +164,10 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ntiles * (uint32_t)KT * 1024u);
   const __amdgpu_buffer_rsrc_t zr = make_rsrc(zb, ntiles * (uint32_t)NG * 8u);
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(sb, ntiles * (uint32_t)NG * 32u);
+  // Zero-length ranges for the prefetches past the k-slice: the loads are
+  // still issued (every wait count assumes a fixed number of loads per
+  // step) but return zeros without a memory access.
+  const __amdgpu_buffer_rsrc_t wr0 = make_rsrc(wb, 0u), zr0 = make_rsrc(zb, 0u), sr0 = make_rsrc(sb, 0u);
   uint32_t woff[NTW], zoff[NTW], soff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
@@ -178,24 +184,29 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Activation k-tile kt (zeros past K), m-tiles [i0, i1), into LDS buffer p.
+  // Activation k-tile kt (zeros past K or past the k-slice), m-tiles
+  // [i0, i1), into LDS buffer p.
   auto load_x = [&](int p, int kt, int i0, int i1) {
-    const bool kval = kt * 128 + wave * 32 < K;  // wave-uniform
+    const bool kval = kt < kend && kt * 128 + wave * 32 < K;  // wave-uniform
     const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
     u32x4* dst = xbuf(p);
 #pragma unroll
     for (int i = i0; i < i1; ++i) load_lds16(r, &dst[(i * 4 + wave) * 64], xoff[i], kt * 256);
   };
+  // Weights, zero words and scales of k-tile kt (zeros past the k-slice).
   auto load_w = [&](WStage<GPT>& S, int kt) {
+    const bool live = kt < kend;  // wave-uniform
+    const __amdgpu_buffer_rsrc_t rw = live ? wr : wr0, rz = live ? zr : zr0, rs = live ? sr : sr0;
+    kt = min(kt, KT - 1);
     const int g0 = (kt * 128) >> a.gshift;  // first group of the k-tile
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      S.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kt * 1024, 0);
+      S.q[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], kt * 1024, 0);
 #pragma unroll
-      for (int g = 0; g < GPT; ++g) S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j] + 8 * g, g0 * 8, 0);
+      for (int g = 0; g < GPT; ++g) S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[j] + 8 * g, g0 * 8, 0);
 #pragma unroll
       for (int g = 0; g < GPT; ++g)
-        S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j] + 32 * g, g0 * 32, 0);
+        S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[j] + 32 * g, g0 * 32, 0);
     }
   };
 
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     fetch(0, st[p], xbuf(p), 2);
     mma(1);
-    load_w(st[pa], min(ka, KT - 1));  // the wait counts rely on this issue order
+    load_w(st[pa], ka);  // the wait counts rely on this issue order
     __builtin_amdgcn_sched_barrier(0);
     fetch(1, st[p], xbuf(p), 3);
     mma(0);
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   for (int p = 0; p + 1 < NS; ++p) {
     load_x(p, kt0 + p, 0, MTL);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(st[p], min(kt0 + p, KT - 1));
+    load_w(st[p], kt0 + p);
     __builtin_amdgcn_sched_barrier(0);
   }
   sync_step();
@@ -283,7 +294,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // Whole rounds of NS k-tiles, then the remaining k-tiles.  A counted loop
   // keeps every step's loads unconditional, so the compiler's wait counts
   // see the true prefetch distance.
-  // (Prefetches past the k-slice load k-tiles that are never computed.)
+  // (Prefetches past the k-slice return zeros that are never computed.)
   int i = 0;
   for (; i + NS <= nsteps; i += NS) {
 #pragma unroll
@@ -312,14 +323,22 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   }
 
   // Split K: this slice's partial tile, in fp32, for the reduction kernel.
-  const int64_t Np = (int64_t)a.NT * 16;
+  // Written through to memory (device-scope stores): no dirty L2 lines are
+  // left for the end-of-kernel writeback that the reduction kernel waits for.
+  // The planner keeps ks * M * Np * 4 below 2^31, so one slice's byte
+  // offsets fit the 32-bit buffer offset.
+  const int Np = a.NT * 16;
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part + (int64_t)kslice * a.M * Np, (uint32_t)a.M * (uint32_t)Np * 4u);
 #pragma unroll
   for (int mt = 0; mt < MTL; ++mt)
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       const int m = mt * 16 + c;
       const int n0 = (nt0 + j) * 16 + 4 * lg;
-      if (m < rows && n0 < Np) *(f32x4*)(a.part + ((int64_t)kslice * a.M + m0 + m) * Np + n0) = acc[mt][j];
+      if (m < rows && n0 < Np)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][j]), pr,
+                                               ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
+                                               kCacheDevice);
     }
 }
 
