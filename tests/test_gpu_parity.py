@@ -402,11 +402,9 @@ def test_every_tiled_variant(bm, G, dtype, monkeypatch):
                                      (24, 4096, 28672, 128), (2048, 8192, 264, 128)])
 def test_tiled_split_k_parity_and_determinism(M, K, N, G):
     """Prefill-kernel grids with fewer output tiles than CUs split K across
-    workgroups.  The last slice to arrive reduces the tile (or, when the
-    grid has more output tiles than the counter buffer holds -- the last
-    case -- a second kernel does), always in slice order: repeated calls and
-    graph replays are bit-identical, and the arrival counters are left at
-    zero."""
+    workgroups; a second kernel sums the slices' fp32 partials in slice
+    order, so repeated calls and graph replays are bit-identical, and the
+    counters are left at zero."""
     ops = _ops()
     assert ops.gemm_kernel(M, N, K, G) == "tiled_kernel"
     assert ops.workspace_bytes(M, N, K, G) > 0
