@@ -273,11 +273,11 @@ struct MoeArgs {
   int mul_rw;
 };
 
-// Workgroup shape: 8 waves, each owning two 16-column tiles (256 columns per
-// workgroup, or 128 gate + 128 up columns with a gate/up activation), so the
-// gathered activation tile in LDS feeds 16 tiles while each wave's prefetch
-// state stays small enough for two workgroups per CU with three k-tiles of
-// loads in flight per wave.
+// Workgroup shape: 8 waves (two per SIMD), each owning two 16-column tiles
+// (256 columns per workgroup, or 128 gate + 128 up columns with a gate/up
+// activation), so the gathered activation tile in LDS feeds 16 tiles; with
+// three k-tiles of loads in flight per wave one workgroup fills a CU's
+// registers.
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTilesPerWave = 2;
