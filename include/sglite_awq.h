@@ -108,6 +108,25 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype,
                    void* ws, int64_t ws_bytes, int32_t* counters, awq_stream_t stream);
 
+/* ---- W4A16 GEMM with the gated activation fused ----------------------------
+ * out[M, N/2] = act(gate) * up, where [gate | up] = x[M, K] @ W (+ bias[N]) are
+ * the two column halves of a merged gate_up projection (gate columns first,
+ * MergedColumnParallelLinear of layers/linear.py:127-143).  Each half is
+ * rounded to the activation dtype (bias added in that dtype) exactly as
+ * awq_w4a16_gemm stores it, then act(gate) * up is computed in fp32 and
+ * rounded once: GatedMLP.forward's gate_up_proj + act_fn
+ * (python/sglite/srt/model_executor/models/blocks.py:51-57; silu_and_mul /
+ * gelu_and_mul of layers/activation.py:11-23) without the [M, N]
+ * intermediate or its second launch.  N % 32 == 0; out 8-byte aligned.
+ * Workspace and counters as for awq_w4a16_gemm, sized by
+ * awq_workspace_bytes_act (no counterpart in the reference: a fusion of
+ * two of its calls). */
+enum { AWQ_ACT_SILU = 1, AWQ_ACT_GELU = 2 };
+int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G);
+int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
+                       int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
+                       int64_t ws_bytes, int32_t* counters, awq_stream_t stream);
+
 /* ---- grouped MoE -------------------------------------------------------------
  * The stages of the fused MoE backend
  * (python/sglite/srt/model_executor/layers/fused_moe/fused.py:101-202) with AWQ

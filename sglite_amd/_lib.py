@@ -42,6 +42,9 @@ SIGNATURES = {
     "awq_counter_bytes": (_i64, [_i64]),
     "awq_gemm_kernel_kind": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp]),
+    "awq_workspace_bytes_act": (_i64, [_i64, _i64, _i64, _i64]),
+    "awq_w4a16_gemm_act": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp,
+                                  _vp]),
     "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i64)]),
     "awq_moe_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
@@ -52,6 +55,9 @@ SIGNATURES = {
                                   _i64, _int, _int, _vp, _vp]),
     "awq_moe_sum_reduce": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp]),
 }
+
+AWQ_ACT_SILU = 1
+AWQ_ACT_GELU = 2
 
 AWQ_MOE_ACT_NONE = 0
 AWQ_MOE_ACT_SILU = 1

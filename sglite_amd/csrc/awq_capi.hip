@@ -13,6 +13,7 @@
 #include <string>
 
 #include "../../include/sglite_awq.h"
+#include "awq_epilogue.h"
 #include "awq_launch.h"
 
 using namespace sgl_awq;
@@ -200,8 +201,57 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
     if (!aligned(ws, 16)) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: workspace must be 16-byte aligned");
     if (!counters) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: split-K needs the counters buffer");
   }
-  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, (hipStream_t)stream),
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
                     "awq_w4a16_gemm launch");
+}
+
+int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative");
+  if (N % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "a gate/up projection needs N %% 32 == 0, got %lld", (long long)N);
+  if (M == 0) return 0;
+  return plan_gemm(make_geom(M, N, K, Gr), kActSilu).ws_bytes;
+}
+
+int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
+                       int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
+                       int64_t ws_bytes, int32_t* counters, awq_stream_t stream) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (activation != AWQ_ACT_SILU && activation != AWQ_ACT_GELU)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: activation must be AWQ_ACT_SILU or AWQ_ACT_GELU, got %d",
+                activation);
+  if (N % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT,
+                "awq_w4a16_gemm_act: N must be a multiple of 32 (two halves of whole 16-column tiles), got %lld",
+                (long long)N);
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative, got %lld", (long long)M);
+  if (M == 0) return ok();
+  if (M > (int64_t(1) << 24)) return fail(AWQ_STATUS_UNSUPPORTED, "M must be below 2^24, got %lld", (long long)M);
+  if (!x || !w || !s || !z || !out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: null pointer argument");
+  if (!aligned(x, 16)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: x must be 16-byte aligned");
+  if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: out must be 8-byte aligned");
+  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: repacked buffers must be 16-byte aligned");
+  if (bias && !aligned(bias, 8))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm_act: bias must be 8-byte aligned");
+  const int act = activation == AWQ_ACT_SILU ? kActSilu : kActGelu;
+  const Geom g = make_geom(M, N, K, Gr);
+  const GemmPlan p = plan_gemm(g, act);
+  if (p.ws_bytes > 0) {
+    if (!ws || ws_bytes < p.ws_bytes)
+      return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: workspace of %lld bytes needed, %lld given",
+                  (long long)p.ws_bytes, (long long)(ws ? ws_bytes : 0));
+    if (!aligned(ws, 16)) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: workspace must be 16-byte aligned");
+    if (!counters) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: split-K needs the counters buffer");
+  }
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, act, (hipStream_t)stream),
+                    "awq_w4a16_gemm_act launch");
 }
 
 int64_t awq_moe_sorted_capacity(int64_t numel, int64_t E, int64_t block_size) {

@@ -62,14 +62,15 @@ bool gemv_preferred(const Geom& g) {
   return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
 }
 
-// 8 waves of at most 4 k-tiles, one column tile per workgroup.
-int gemv_default_variant(const Geom&) { return 11084; }
+// 8 waves of at most 4 k-tiles, one column tile per workgroup (with a fused
+// gate/up activation: one gate tile and its up tile per workgroup).
+int gemv_default_variant(const Geom&, int act) { return act ? 21084 : 11084; }
 
-bool plan_gemv(const Geom& g, GemmPlan& p) {
+bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
   if (g.NG > 1 && g.G < 128) return false;
-  int v = gemv_default_variant(g);
+  int v = gemv_default_variant(g, act);
   const int env = env_int("SGL_AWQ_GEMV_VARIANT", 0);
-  if (gemv_variant_ok(env)) v = env;
+  if (gemv_variant_ok(env) && (!act || env / 10000 == 2)) v = env;
   if (!gemv_variant_ok(v)) return false;
   const int ntw = v / 10000, wn = (v / 1000) % 10, wk = (v / 10) % 100, kpw = v % 10;
   const int64_t mt = (g.M + 15) / 16, threads = 64 * wn * wk;
@@ -115,10 +116,10 @@ bool tiled_preferred(const Geom& g) {
   return g.M == 16 && g.N >= 16384 && kn >= 20000000;
 }
 
-GemmPlan plan_gemm(const Geom& g) {
+GemmPlan plan_gemm(const Geom& g, int act) {
   GemmPlan p{};
   const bool tiled = tiled_preferred(g);
-  if (!tiled && gemv_preferred(g) && plan_gemv(g, p)) return p;
+  if (!tiled && gemv_preferred(g) && plan_gemv(g, p, act)) return p;
   if (!tiled) {
     p.kind = 0;
     // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all
@@ -139,8 +140,13 @@ GemmPlan plan_gemm(const Geom& g) {
     } else {
       wk = g.M <= 8 ? 4 : (g.M <= 16 ? 8 : 16);
     }
+    if (act && ntw != 2) {  // a fused gate/up pair needs two tiles per wave
+      ntw = 2;
+      wn = 2;
+      wk = g.M <= 16 ? 4 : 2;
+    }
     const int env = env_int("SGL_AWQ_SKINNY_VARIANT", 0);
-    if (skinny_variant_ok(env)) {
+    if (skinny_variant_ok(env) && (!act || env / 10000 == 2)) {
       ntw = env / 10000;
       wn = (env / 100) % 100;
       wk = env % 100;
@@ -211,11 +217,11 @@ GemmPlan plan_gemm(const Geom& g) {
 }
 
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                        hipStream_t s) {
-  if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
-  if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
-  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, s);
+  if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
+  if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
+  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
 }
 
 }  // namespace sgl_awq

@@ -35,12 +35,110 @@ namespace sgl_awq {
 
 namespace {
 
+// Epilogue of a gemv workgroup with a fused gate/up activation: wave wn
+// holds gate tile t = blockIdx.x * WN + wn in slot 0 and its up tile
+// t + NT / 2 in slot 1.  Pair-quad pq = (wn' * MT + mt) * 64 + l covers row
+// 16 mt + l % 16 and output columns 16 t' + 4 (l / 16) .. + 3 of both tiles.
+// With WK > 1 the k-waves' sums are in red (quad ((wn' * MT + mt) * 2 + slot)
+// * 64 + l of k-wave o at red[o * NQ + quad]); split K publishes both tiles'
+// partials at their physical columns and the last workgroup applies the
+// activation to the slice sums.
+template <int WN, int WK, int MT, int NTHREADS, typename DT>
+__device__ __forceinline__ void gemv_paired_epilogue(const f32x4 (&acc)[MT][2], const f32x4* red,
+                                                     const typename DT::elem* __restrict__ bias,
+                                                     typename DT::elem* __restrict__ out, float* __restrict__ part,
+                                                     int32_t* __restrict__ counters, int M, int N, int NT, int KS,
+                                                     int act, int wn, int lane) {
+  constexpr int NQ = WN * MT * 2 * 64;
+  constexpr int NP = WN * MT * 64;
+  constexpr int NU = WK > 1 ? (NP + NTHREADS - 1) / NTHREADS : MT;
+  const int NTg = NT >> 1, Nh = N >> 1;
+  const int64_t Np = (int64_t)NT * 16;
+  auto pos = [&](int u, int& m, int& tq, int& c4) {
+    const int pq = WK > 1 ? (int)threadIdx.x + u * NTHREADS : (wn * MT + u) * 64 + lane;
+    const int l = pq & 63, r = pq >> 6;
+    m = (r % MT) * 16 + (l & 15);
+    tq = blockIdx.x * WN + r / MT;
+    c4 = 4 * (l >> 4);
+    return pq < NP;
+  };
+  auto vals = [&](int u, f32x4& g, f32x4& v) {
+    if constexpr (WK > 1) {
+      const int pq = min((int)threadIdx.x + u * NTHREADS, NP - 1);
+      const int qg = (pq >> 6) * 128 + (pq & 63);
+      g = red[qg];
+      v = red[qg + 64];
+#pragma unroll
+      for (int o = 1; o < WK; ++o) {
+        g += red[o * NQ + qg];
+        v += red[o * NQ + qg + 64];
+      }
+    } else {
+      g = acc[u][0];
+      v = acc[u][1];
+    }
+  };
+  if (KS == 1) {
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      int m, tq, c4;
+      if (pos(u, m, tq, c4) && m < M && tq < NTg) {
+        f32x4 g, v;
+        vals(u, g, v);
+        store4_act<DT>(out, bias, m, Nh, tq * 16 + c4, Nh, g, v, act);
+      }
+    }
+    return;
+  }
+  float chk = 0.f;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    int m, tq, c4;
+    if (pos(u, m, tq, c4) && m < M && tq < NTg) {
+      f32x4 g, v;
+      vals(u, g, v);
+      float* pg = part + ((int64_t)blockIdx.y * M + m) * Np + tq * 16 + c4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        chk += xchg_agent(pg + r, g[r]);
+        chk += xchg_agent(pg + Nh + r, v[r]);
+      }
+    }
+  }
+  asm volatile("" ::"v"(chk));
+  __syncthreads();
+  __shared__ int s_last;
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&counters[blockIdx.x], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == KS - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    int m, tq, c4;
+    if (pos(u, m, tq, c4) && m < M && tq < NTg) {
+      f32x4 g = f32x4{0.f, 0.f, 0.f, 0.f}, v = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        float* pg = part + ((int64_t)ks * M + m) * Np + tq * 16 + c4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          g[r] += xchg_agent(pg + r, 0.f);
+          v[r] += xchg_agent(pg + Nh + r, 0.f);
+        }
+      }
+      store4_act<DT>(out, bias, m, Nh, tq * 16 + c4, Nh, g, v, act);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int NTW, int WN, int WK, int KPW, int MT, int XPT, typename DT>
 __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
     const uint64_t* __restrict__ z_r, const typename DT::elem* __restrict__ bias, typename DT::elem* __restrict__ out,
     float* __restrict__ part, int32_t* __restrict__ counters, int M, int N, int K, int NT, int KT, int NG, int gshift,
-    int ktc, int KS) {
+    int ktc, int KS, int act) {
   using V8 = typename DT::vec8;
   using ZS = typename Dq<DT>::ZS;
   constexpr int NTHREADS = 64 * WN * WK;
@@ -77,10 +175,15 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   u32x4 q[KPW][NTW];
   uint32_t zw[KPW][NTW];
   uint16_t sb[KPW][NTW];
+  // With a fused gate/up activation (two tiles per wave) the wave's tiles
+  // are gate tile t = blockIdx.x * WN + wn and its up tile t + NT / 2.
+  const bool paired = NTW == 2 && act != kActNone;
+  const int tpair = blockIdx.x * WN + wn;
   uint32_t woff[NTW], goff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    const uint32_t ntc = (uint32_t)min(nt0 + j, NT - 1);  // columns past N read a valid tile, never stored
+    // columns past N read a valid tile, never stored
+    const uint32_t ntc = (uint32_t)(paired ? min(tpair, (NT >> 1) - 1) + j * (NT >> 1) : min(nt0 + j, NT - 1));
     woff[j] = (ntc * (uint32_t)KT * 64u + lane) * 16u;
     goff[j] = ntc * (uint32_t)NG;
   }
@@ -167,6 +270,14 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     }
   }
 
+  if constexpr (NTW == 2) {
+    if (paired) {
+      gemv_paired_epilogue<WN, WK, MT, NTHREADS, DT>(acc, (const f32x4*)smem, bias, out, part, counters, M, N, NT, KS,
+                                                    act, wn, lane);
+      return;
+    }
+  }
+
   // Output quad of this thread: with WK > 1 thread t owns quads t + u*NTHREADS;
   // with WK == 1 each lane keeps its own accumulators.
   auto quad_pos = [&](int u, int& m, int& n0) {
@@ -240,7 +351,8 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
 
 template <typename DT>
 hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                          const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, hipStream_t s) {
+                          const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, int act,
+                          hipStream_t s) {
   using E = typename DT::elem;
   const uint16_t* sbase = (const uint16_t*)sr;
   const uint64_t* zbase = (const uint64_t*)zr;
@@ -253,7 +365,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   if (ntw == NTW_ && wn == WN_ && wk == WK_ && kpw == KPW_ && mt == MT_ && xpt == XPT_) {                          \
     hipLaunchKernelGGL((gemv_kernel<NTW_, WN_, WK_, KPW_, MT_, XPT_, DT>), grid, dim3(64 * WN_ * WK_), lds, s,       \
                        (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters,  \
-                       (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks);      \
+                       (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks, act); \
     return hipGetLastError();                                                                                     \
   }
 #define SGL_GEMV_X(NTW_, WN_, WK_, KPW_, MT_) \
@@ -263,6 +375,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   SGL_GEMV_M(1, 1, 4, 8)
   SGL_GEMV_M(1, 1, 8, 4)
   SGL_GEMV_M(2, 1, 4, 4)
+  SGL_GEMV_M(2, 1, 8, 4)
   SGL_GEMV_M(2, 2, 2, 8)
   SGL_GEMV_M(2, 2, 4, 4)
   SGL_GEMV_M(2, 4, 2, 4)
@@ -279,7 +392,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
 // Variant code: ntw * 10000 + wn * 1000 + wk * 10 + kpw.
 bool gemv_variant_ok(int v) {
   switch (v) {
-    case 11048: case 11084: case 21044: case 22028: case 22044: case 24024: case 24042: case 14044:
+    case 11048: case 11084: case 21044: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
       return true;
     default:
       return false;
@@ -287,10 +400,10 @@ bool gemv_variant_ok(int v) {
 }
 
 hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                        hipStream_t s) {
-  return dtype == 0 ? launch_gemv_dt<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, s)
-                    : launch_gemv_dt<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, s);
+  return dtype == 0 ? launch_gemv_dt<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, act, s)
+                    : launch_gemv_dt<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, act, s);
 }
 
 }  // namespace sgl_awq

@@ -35,20 +35,22 @@ struct GemmPlan {
   int64_t lds_bytes;  // dynamic LDS (GEMV)
 };
 
-GemmPlan plan_gemm(const Geom& g);
+// act: fused gate/up activation of the output (0 none, 1 silu, 2 gelu; the
+// GEMM's two column halves are gate and up, the output has N / 2 columns).
+GemmPlan plan_gemm(const Geom& g, int act = 0);
 hipError_t launch_skinny(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                          hipStream_t s);
 bool gemv_variant_ok(int v);
 hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                        hipStream_t s);
 int64_t tiled_max_k(int bm);
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                         hipStream_t s);
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                        hipStream_t s);
 
 // Grouped MoE path (awq_moe.hip).

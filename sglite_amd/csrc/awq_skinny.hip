@@ -47,7 +47,7 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
     const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
     const uint64_t* __restrict__ z_r, const typename DT::elem* __restrict__ bias, typename DT::elem* __restrict__ out,
     float* __restrict__ part, int32_t* __restrict__ counters, int M, int N, int K, int NT, int KT, int NG, int gshift,
-    int ktc, int KS) {
+    int ktc, int KS, int act) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
   using V4 = typename DT::vec4;
@@ -100,10 +100,16 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
   uint32_t xoff[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xoff[mt] = ((uint32_t)min(mt * 16 + c, M - 1) * (uint32_t)K + lg * 8) * 2u;
+  // With a fused gate/up activation (two tiles per wave) the wave's tiles
+  // are gate tile t = blockIdx.x * WN + wn and its up tile t + NT / 2.
+  const bool paired = NTW == 2 && act != kActNone;
+  const int NTg = NT >> 1, Nh = N >> 1;
+  const int tpair = blockIdx.x * WN + wn;
   uint32_t woff[NTW], srow_off[NTW], sown_off[NTW], zoff[NTW];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    const uint32_t ntc = (uint32_t)min(nt0 + j, NT - 1);  // columns past N read a valid tile, never stored
+    // columns past N read a valid tile, never stored
+    const uint32_t ntc = (uint32_t)(paired ? min(tpair, NTg - 1) + j * NTg : min(nt0 + j, NT - 1));
     woff[j] = (ntc * (uint32_t)KT * 64u + lane) * 16u;
     srow_off[j] = (ntc * (uint32_t)NG * 16u + 4u * lg) * 2u;  // scales of output rows 4lg..4lg+3
     sown_off[j] = (ntc * (uint32_t)NG * 16u + c) * 2u;        // scale of the lane's own column
@@ -261,6 +267,19 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
   }
 
   // Output fragment of (mt, j): row m = 16*mt + c, columns n0..n0+3.
+  if (KS == 1 && paired) {
+    if constexpr (NTW == 2) {
+      if (wk == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + c;
+          if (m < M && tpair < NTg)
+            store4_act<DT>(out, bias, m, Nh, tpair * 16 + 4 * lg, Nh, acc[mt][0], acc[mt][1], act);
+        }
+      }
+    }
+    return;
+  }
   if (KS == 1) {
     if (wk == 0) {
 #pragma unroll
@@ -283,8 +302,11 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
         const int m = mt * 16 + c;
-        const int n0 = (nt0 + j) * 16 + 4 * lg;
-        if (m < M && n0 < Np) {
+        // physical column of the fragment (a fused gate/up pair keeps the up
+        // tile's partials at its own column, Nh further on)
+        const int n0 = (paired ? (tpair + j * NTg) : (nt0 + j)) * 16 + 4 * lg;
+        const bool val = paired ? tpair < NTg : n0 < Np;
+        if (m < M && val) {
           float* p = part + ((int64_t)blockIdx.y * M + m) * Np + n0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) chk += xchg_agent(p + r, acc[mt][j][r]);
@@ -303,6 +325,28 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
   __syncthreads();
   if (!s_last) return;
 
+  if (paired) {
+    // Output quads of the workgroup's WN pairs: gate partial column o0, up o0 + Nh.
+    constexpr int QPP = WN * 4;
+    for (int idx = threadIdx.x; idx < M * QPP; idx += NTHREADS) {
+      const int m = idx / QPP, qq = idx % QPP;
+      const int tq = blockIdx.x * WN + qq / 4;
+      if (tq >= NTg) continue;
+      const int64_t o0 = (int64_t)tq * 16 + 4 * (qq % 4);
+      f32x4 g = f32x4{0.f, 0.f, 0.f, 0.f}, v = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        float* p = part + ((int64_t)ks * M + m) * Np + o0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          g[r] += xchg_agent(p + r, 0.f);
+          v[r] += xchg_agent(p + Nh + r, 0.f);
+        }
+      }
+      store4_act<DT>(out, bias, m, Nh, o0, Nh, g, v, act);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   constexpr int QPR = NTG * 4;  // float4 quads per row of this column group
   const int64_t nbase = (int64_t)blockIdx.x * NTG * 16;
   for (int idx = threadIdx.x; idx < M * QPR; idx += NTHREADS) {
@@ -322,7 +366,7 @@ __global__ __launch_bounds__(64 * WN * WK) void skinny_kernel(
 
 template <typename DT>
 hipError_t launch_skinny_dt_impl(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                                 const void* bias, void* out, const Geom& g, void* ws, int32_t* counters,
+                                 const void* bias, void* out, const Geom& g, void* ws, int32_t* counters, int act,
                                  hipStream_t s) {
   using E = typename DT::elem;
   const uint16_t* sbase = (const uint16_t*)sr;
@@ -336,7 +380,7 @@ hipError_t launch_skinny_dt_impl(const GemmPlan& p, const void* x, const void* w
     hipLaunchKernelGGL((skinny_kernel<MT_, NTW_, WN_, WK_, GPT_, DT>), grid, dim3(64 * WN_ * WK_), 0, s,     \
                        (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws,       \
                        counters, (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, \
-                       p.ks);                                                                                \
+                       p.ks, act);                                                                           \
     return hipGetLastError();                                                                                \
   }
 #define SGL_SKINNY_G(MT_, NTW_, WN_, WK_) \
@@ -360,10 +404,10 @@ hipError_t launch_skinny_dt_impl(const GemmPlan& p, const void* x, const void* w
 }  // namespace
 
 hipError_t launch_skinny(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                          hipStream_t s) {
-  return dtype == 0 ? launch_skinny_dt_impl<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, s)
-                    : launch_skinny_dt_impl<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, s);
+  return dtype == 0 ? launch_skinny_dt_impl<F16>(p, x, w, sr, zr, bias, out, g, ws, counters, act, s)
+                    : launch_skinny_dt_impl<BF16>(p, x, w, sr, zr, bias, out, g, ws, counters, act, s);
 }
 
 }  // namespace sgl_awq

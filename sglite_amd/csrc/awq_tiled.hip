@@ -75,6 +75,7 @@ struct TiledArgs {
   int M, N, K, NT, KT, NG, gshift;
   int gx, gy;  // column blocks (256 columns), row blocks (BM rows)
   int ks, ktc;  // k-slices and k-tiles per slice
+  int act;      // fused gate/up activation (kActNone: plain GEMM)
 };
 
 // Workgroup id -> (column block, row block).  Ids b, b + 8, b + 16, ... run
@@ -151,31 +152,45 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   for (int i = 0; i < MTL; ++i)
     xoff[i] = (uint32_t)min(i * 16 + c, rows - 1) * (uint32_t)K * 2u + (uint32_t)(wave * 64 + lg * 16);
 
-  // Weights, zeros and scales of this wave's four column tiles (the last
-  // ones clamp to the final tile; their columns are never stored).
+  // Weights, zeros and scales of this wave's four column tiles, as two pairs
+  // of adjacent tiles: tiles nt0 .. nt0 + 3, or with a fused gate/up
+  // activation gate tiles t, t + 1 and their up tiles t + NT / 2, t + 1 + NT / 2
+  // (the merged projection's halves), so one lane holds a gate and its up
+  // column.  Tiles past the end clamp to the last tile; their columns are never
+  // stored.  Each pair has its own buffer range, ending at its last real tile.
   const int nt0 = bx * 16 + wave * NTW;
-  const int ntb = min(nt0, a.NT - 1);
-  const u32x4* wb = a.w + (int64_t)ntb * KT * 64;
-  const uint64_t* zb = a.z + (int64_t)ntb * NG;
-  const uint16_t* sb = a.s + (int64_t)ntb * NG * 16;
-  // Buffer ranges end at the wave's last real tile, so the reads of groups
-  // past K in a partial last k-tile (G < 128) return zeros.
-  const uint32_t ntiles = (uint32_t)min(NTW, a.NT - ntb);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(wb, ntiles * (uint32_t)KT * 1024u);
-  const __amdgpu_buffer_rsrc_t zr = make_rsrc(zb, ntiles * (uint32_t)NG * 8u);
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(sb, ntiles * (uint32_t)NG * 32u);
-  // Zero-length ranges for the prefetches past the k-slice: the loads are
-  // still issued (every wait count assumes a fixed number of loads per
-  // step) but return zeros without a memory access.
-  const __amdgpu_buffer_rsrc_t wr0 = make_rsrc(wb, 0u), zr0 = make_rsrc(zb, 0u), sr0 = make_rsrc(sb, 0u);
-  uint32_t woff[NTW], zoff[NTW], soff[NTW];
+  const int NTg = a.NT >> 1;
+  const int pb0 = a.act ? (nt0 >> 1) : nt0;               // first tile of pair 0
+  const int pb1 = a.act ? (nt0 >> 1) + NTg : nt0 + 2;     // first tile of pair 1
+  int pt[NTW];  // physical tile of slot j
+  bool pv[NTW];  // slot j's columns are stored
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    const uint32_t dt = (uint32_t)(min(nt0 + j, a.NT - 1) - ntb);
-    woff[j] = dt * (uint32_t)KT * 1024u + (uint32_t)lane * 16u;
-    zoff[j] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
-    soff[j] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+    pt[j] = (j < 2 ? pb0 : pb1) + (j & 1);
+    pv[j] = a.act ? (nt0 >> 1) + (j & 1) < NTg : pt[j] < a.NT;
   }
+  __amdgpu_buffer_rsrc_t wr[2], zr[2], sr[2];
+  uint32_t woff[NTW], zoff[NTW], soff[NTW];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int base = min(q == 0 ? pb0 : pb1, a.NT - 1);
+    const uint32_t ntiles = (uint32_t)min(2, a.NT - base);
+    wr[q] = make_rsrc(a.w + (int64_t)base * KT * 64, ntiles * (uint32_t)KT * 1024u);
+    zr[q] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
+    sr[q] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * q + h;
+      const uint32_t dt = (uint32_t)(min(pt[j], a.NT - 1) - base);
+      woff[j] = dt * (uint32_t)KT * 1024u + (uint32_t)lane * 16u;
+      zoff[j] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
+      soff[j] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+    }
+  }
+  // Zero-length range for the prefetches past the k-slice: the loads are
+  // still issued (every wait count assumes a fixed number of loads per
+  // step) but return zeros without a memory access.
+  const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.w, 0u);
   const uint32_t zshift = 4u * (uint32_t)(c & 7);
 
   f32x4 acc[MTL][NTW];
@@ -196,11 +211,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // Weights, zero words and scales of k-tile kt (zeros past the k-slice).
   auto load_w = [&](WStage<GPT>& S, int kt) {
     const bool live = kt < kend;  // wave-uniform
-    const __amdgpu_buffer_rsrc_t rw = live ? wr : wr0, rz = live ? zr : zr0, rs = live ? sr : sr0;
     kt = min(kt, KT - 1);
     const int g0 = (kt * 128) >> a.gshift;  // first group of the k-tile
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
+      const __amdgpu_buffer_rsrc_t rw = live ? wr[j >> 1] : r0, rz = live ? zr[j >> 1] : r0,
+                                   rs = live ? sr[j >> 1] : r0;
       S.q[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], kt * 1024, 0);
 #pragma unroll
       for (int g = 0; g < GPT; ++g) S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[j] + 8 * g, g0 * 8, 0);
@@ -311,14 +327,26 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   const E* bias = (const E*)a.bias;
   E* out = (E*)a.out;
   if (a.ks == 1) {
+    if (a.act == kActNone) {
 #pragma unroll
-    for (int mt = 0; mt < MTL; ++mt)
+      for (int mt = 0; mt < MTL; ++mt)
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) {
-        const int m = mt * 16 + c;
-        const int n0 = (nt0 + j) * 16 + 4 * lg;
-        if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, acc[mt][j]);
-      }
+        for (int j = 0; j < NTW; ++j) {
+          const int m = mt * 16 + c;
+          const int n0 = pt[j] * 16 + 4 * lg;
+          if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, acc[mt][j]);
+        }
+    } else {
+      const int Nh = a.N >> 1;
+#pragma unroll
+      for (int mt = 0; mt < MTL; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int m = mt * 16 + c;
+          if (m < rows && pv[j])
+            store4_act<DT>(out, bias, (int64_t)m0 + m, Nh, pt[j] * 16 + 4 * lg, Nh, acc[mt][j], acc[mt][j + 2], a.act);
+        }
+    }
     return;
   }
 
@@ -334,8 +362,8 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       const int m = mt * 16 + c;
-      const int n0 = (nt0 + j) * 16 + 4 * lg;
-      if (m < rows && n0 < Np)
+      const int n0 = pt[j] * 16 + 4 * lg;
+      if (m < rows && pv[j])
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][j]), pr,
                                                ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
                                                kCacheDevice);
@@ -343,32 +371,44 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 }
 
 // Sum of the k-slices' partials in slice order (deterministic), plus bias, in
-// the output dtype.  One thread per four output columns; the slices are read
+// the output dtype (with a fused gate/up activation: gate and up sums, then
+// act(gate) * up).  One thread per four output columns; the slices are read
 // four at a time, all four loads in flight (slices past ks read as zeros
 // through the buffer range).
 template <typename DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
                                                             const typename DT::elem* __restrict__ bias,
                                                             typename DT::elem* __restrict__ out, int M, int N,
-                                                            int Np, int ks) {
-  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t m = q / (N / 4);
-  const int64_t n0 = 4 * (q - m * (N / 4));
-  if (m >= M) return;
+                                                            int Np, int ks, int act) {
   const uint32_t slice = (uint32_t)M * (uint32_t)Np * 4u;  // bytes per k-slice
   const __amdgpu_buffer_rsrc_t r = make_rsrc(part, slice * (uint32_t)ks);
+  // Sum of four consecutive partial columns starting at byte offset off.
+  auto sum4 = [&](uint32_t off) {
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < ks; k += 4) {
+      f32x4 v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + (uint32_t)i * slice,
+                                                                                (int)((uint32_t)k * slice), 0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum += v[i];
+    }
+    return sum;
+  };
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int No = act == kActNone ? N : N / 2;  // output columns
+  const int64_t m = q / (No / 4);
+  const int64_t n0 = 4 * (q - m * (No / 4));
+  if (m >= M) return;
   const uint32_t off = ((uint32_t)m * (uint32_t)Np + (uint32_t)n0) * 4u;
-  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < ks; k += 4) {
-    f32x4 v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + (uint32_t)i * slice,
-                                                                              (int)((uint32_t)k * slice), 0));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sum += v[i];
+  if (act == kActNone) {
+    store4<DT>(out, bias, m, N, n0, sum4(off));
+  } else {
+    // Gate column n0 and its up column n0 + N / 2 (both in the partials).
+    const f32x4 g = sum4(off), u = sum4(off + (uint32_t)(N / 2) * 4u);
+    store4_act<DT>(out, bias, m, No, n0, No, g, u, act);
   }
-  store4<DT>(out, bias, m, N, n0, sum);
 }
 
 template <int BM, typename DT>
@@ -401,7 +441,7 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
 int64_t tiled_max_k(int bm) { return ((int64_t(1) << 31) - 1) / (2 * (int64_t)bm); }
 
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                         hipStream_t s) {
   if (p.grid_x * p.grid_y * p.ks >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
   TiledArgs a;
@@ -423,18 +463,19 @@ hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const v
   a.ks = p.ks;
   a.ktc = p.ktc;
   a.part = (float*)ws;
+  a.act = act;
   // Groups per 128-row k-tile: 1 for G >= 128 (or one group), else 128 / G.
   const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
   hipError_t e = dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
   if (e != hipSuccess || p.ks == 1) return e;
-  const int64_t quads = g.M * (g.N / 4);
+  const int64_t quads = g.M * ((act == kActNone ? g.N : g.N / 2) / 4);
   const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
   if (dtype == 0)
     hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, block, 0, s, (const float*)ws, (const _Float16*)bias,
-                       (_Float16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks);
+                       (_Float16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks, act);
   else
     hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, block, 0, s, (const float*)ws, (const __bf16*)bias,
-                       (__bf16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks);
+                       (__bf16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks, act);
   return hipGetLastError();
 }
 

@@ -162,14 +162,31 @@ def make_counters(N: int, device: torch.device) -> torch.Tensor:
     return torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
 
 
+def workspace_bytes_act(M: int, N: int, K: int, group_size: int) -> int:
+    """Split-K workspace of ``gemm(..., activation=...)`` (its plan pairs gate and up tiles)."""
+    G = resolve_group_size(group_size, K)
+    return _lib.check(_lib.load().awq_workspace_bytes_act(M, N, K, G), "awq_workspace_bytes_act")
+
+
+_GATED_ACT = {"silu": _lib.AWQ_ACT_SILU, "gelu": _lib.AWQ_ACT_GELU}
+
+
 def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Optional[torch.Tensor] = None,
-         counters: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[M, N] = rnd(x[M, K] @ W) (+ bias), fp32 accumulation, on x's current stream."""
+         counters: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+         activation: Optional[str] = None) -> torch.Tensor:
+    """out[M, N] = rnd(x[M, K] @ W) (+ bias), fp32 accumulation, on x's current stream.
+
+    With ``activation`` ("silu" or "gelu") the two column halves of W are a
+    merged gate/up projection and the output is ``act(gate) * up``, [M, N / 2],
+    each half rounded (bias added) as the plain GEMM stores it, then the
+    product in fp32, rounded once."""
     _require_cuda(x, r.w)
     if x.dim() != 2 or x.shape[1] != K:
         raise ValueError(f"x must be [M, {K}], got {tuple(x.shape)}")
     if x.dtype != r.s.dtype:
         raise ValueError(f"activation dtype {x.dtype} does not match the scale dtype {r.s.dtype}")
+    if activation is not None and activation not in _GATED_ACT:
+        raise ValueError(f"unsupported activation {activation!r}")
     G = resolve_group_size(group_size, K)
     M = x.shape[0]
     dev = x.device
@@ -179,16 +196,25 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
         if bias.numel() != N:
             raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
         bias = _aligned(bias.to(x.dtype).reshape(-1), 8)
+    ncols = N if activation is None else N // 2
     if out is None:
-        out = torch.empty((M, N), dtype=x.dtype, device=dev)
+        out = torch.empty((M, ncols), dtype=x.dtype, device=dev)
     lib = _lib.load()
-    wsb = workspace_bytes(M, N, K, G) if M > 0 else 0
+    if M > 0:
+        wsb = workspace_bytes(M, N, K, G) if activation is None else workspace_bytes_act(M, N, K, G)
+    else:
+        wsb = 0
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev) if wsb > 0 else None
     if wsb > 0 and counters is None:
         raise ValueError("this shape splits K across workgroups: pass the layer's counters (make_counters)")
-    _lib.check(lib.awq_w4a16_gemm(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
-                                  out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _ptr(ws), wsb, _ptr(counters),
-                                  _stream(dev)), "awq_w4a16_gemm")
+    if activation is None:
+        _lib.check(lib.awq_w4a16_gemm(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
+                                      out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _ptr(ws), wsb, _ptr(counters),
+                                      _stream(dev)), "awq_w4a16_gemm")
+    else:
+        _lib.check(lib.awq_w4a16_gemm_act(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
+                                          out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _GATED_ACT[activation],
+                                          _ptr(ws), wsb, _ptr(counters), _stream(dev)), "awq_w4a16_gemm_act")
     return out
 
 

@@ -1,0 +1,119 @@
+"""GPU parity of the GEMM with the gated activation fused (awq_w4a16_gemm_act):
+out = act(gate) * up over the two column halves of a merged gate/up
+projection, against the oracle's fp32-accumulated GEMM (each half rounded,
+bias added in the activation dtype) followed by silu_and_mul / gelu_and_mul in
+fp32, rounded once: max|err| <= 2e-2 * max|ref|.  Every kernel that can hold a
+gate tile and its up tile together is driven: the small-batch GEMV (every
+two-tile shape), the decode kernel (every two-tile shape), the prefill kernel
+(every row block), with and without split K; fp16 and bf16, silu and gelu,
+with and without bias, and an odd number of gate tiles (the last workgroup
+holds half a pair set)."""
+
+import pytest
+import torch
+
+from oracle import awq_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = 2e-2
+
+
+def _ops():
+    from sglite_amd import ops
+
+    return ops
+
+
+def _reference(x, t, G, bias, act):
+    y = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], bias, G)
+    return oracle._ACT[act](y).to(x.dtype)
+
+
+def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env=None, monkeypatch=None,
+           kernel=None, seed=0):
+    ops = _ops()
+    N = 2 * I
+    t = oracle.make_awq_linear(K, N, G, seed=seed + M + K, dtype=dtype)
+    r = ops.repack(t["qweight"].to(DEV), t["qzeros"].to(DEV), t["scales"].to(DEV))
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(seed + 7)).to(dtype) if with_bias else None
+    for k, v in (env or {}).items():
+        monkeypatch.setenv(k, str(v))
+    if kernel is not None:
+        assert ops.gemm_kernel(M, N, K, G) == kernel
+    cnt = ops.make_counters(N, DEV)
+    x = oracle.make_activation(M, K, seed=seed + 3, dtype=dtype)
+    y = ops.gemm(x.to(DEV), r, K, N, G, bias=None if bias is None else bias.to(DEV), counters=cnt, activation=act)
+    assert tuple(y.shape) == (M, I)
+    ref = _reference(x, t, G, bias, act)
+    ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+    assert ok, (M, K, I, G, dtype, act, env, err, mx)
+    assert int(cnt.abs().sum()) == 0
+    return y
+
+
+@pytest.mark.parametrize("M,K,I,kernel", [
+    (1, 2048, 1040, "gemv_kernel"),     # one slice per workgroup
+    (1, 8192, 1040, "gemv_kernel"),     # split K
+    (4, 2560, 528, "gemv_kernel"),
+    (12, 2048, 1040, "skinny_kernel"),  # split K
+    (24, 2048, 1040, "skinny_kernel"),
+    (16, 1024, 9728, "skinny_kernel"),  # wide: two-tile shapes by default
+    (40, 2048, 1040, "tiled_kernel"),   # split K
+    (300, 1024, 528, "tiled_kernel"),
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_silu_matches_oracle(M, K, I, kernel, dtype, monkeypatch):
+    _check(M, K, I, dtype=dtype, kernel=kernel, monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+@pytest.mark.parametrize("M", [1, 12, 64])
+def test_fused_activation_with_bias(act, M, monkeypatch):
+    _check(M, 1024, 272, act=act, with_bias=True, monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("variant", [21044, 21084, 22028, 22044, 24024, 24042])
+@pytest.mark.parametrize("M", [1, 8])
+def test_every_two_tile_gemv_shape(variant, M, monkeypatch):
+    _check(M, 4096, 1040, env={"SGL_AWQ_GEMV_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 8}, kernel="gemv_kernel",
+           monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("variant", [20202, 20401, 20204])
+@pytest.mark.parametrize("M", [3, 20])
+def test_every_two_tile_decode_shape(variant, M, monkeypatch):
+    _check(M, 4096, 1040, env={"SGL_AWQ_SKINNY_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 0}, kernel="skinny_kernel",
+           monkeypatch=monkeypatch)
+
+
+@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("ks", [1, 3])
+@pytest.mark.parametrize("G", [64, 128, -1])
+def test_every_prefill_row_block(bm, ks, G, monkeypatch):
+    K = 1280 if G != -1 else 1152
+    _check(70, K, 1040, G=G, env={"SGL_AWQ_TILED_BM": bm, "SGL_AWQ_TILED_KS": ks, "SGL_AWQ_TILED_MIN_M": 1},
+           kernel="tiled_kernel", monkeypatch=monkeypatch)
+
+
+def test_fused_equals_unfused_gemm_then_activation(monkeypatch):
+    """Same kernel and plan with and without the activation: the fused output
+    is the plain GEMM's rounded output run through silu in fp32 (prefill
+    kernel, no split K), to within one fp16 ulp of the product (the device's
+    exp and torch's may differ in the last fp32 bit)."""
+    ops = _ops()
+    M, K, I, G = 256, 2048, 2048, 128
+    N = 2 * I
+    t = oracle.make_awq_linear(K, N, G, seed=11)
+    r = ops.repack(t["qweight"].to(DEV), t["qzeros"].to(DEV), t["scales"].to(DEV))
+    monkeypatch.setenv("SGL_AWQ_TILED_KS", "1")  # one k-slice: both calls store straight from the accumulators
+    assert ops.workspace_bytes(M, N, K, G) == 0 and ops.workspace_bytes_act(M, N, K, G) == 0
+    x = oracle.make_activation(M, K, seed=12).to(DEV)
+    y = ops.gemm(x, r, K, N, G).float()
+    fused = ops.gemm(x, r, K, N, G, activation="silu").float()
+    g, u = y[:, :I], y[:, I:]
+    ref = (g / (1.0 + torch.exp(-g)) * u).to(torch.float16).float()
+    ulp = torch.clamp(ref.abs(), min=2.0 ** -14) * 2.0 ** -10
+    assert bool(((fused - ref).abs() <= ulp).all())
+    assert (fused == ref).float().mean().item() > 0.99

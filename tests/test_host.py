@@ -120,6 +120,27 @@ def test_missing_workspace_is_reported_before_launch():
     assert st == _lib.AWQ_STATUS_WORKSPACE and "counters" in _lib.last_error()
 
 
+def test_fused_activation_entry_validates_before_launch():
+    lib = _lib.load()
+    fake = 0x10000  # never dereferenced: validation fails first
+    args = (fake, fake, fake, fake, None, fake)
+    assert lib.awq_w4a16_gemm_act(*args, 4, 64, 256, 128, 0, 3, None, 0, None, None) == -1
+    assert "activation" in _lib.last_error()
+    assert lib.awq_w4a16_gemm_act(*args, 4, 48, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None) == -1
+    assert "multiple of 32" in _lib.last_error()
+    assert lib.awq_w4a16_gemm_act(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, _lib.AWQ_ACT_GELU, None, 0,
+                                  None, None) == -1
+    assert "null" in _lib.last_error()
+    assert lib.awq_w4a16_gemm_act(*args, 0, 64, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None) == 0
+    assert lib.awq_workspace_bytes_act(4, 48, 256, 128) == -1
+    # a gate/up projection narrow enough to split K needs the workspace and the counters
+    M, N, K = 1, 512, 8192
+    need = lib.awq_workspace_bytes_act(M, N, K, 128)
+    assert need > 0
+    st = lib.awq_w4a16_gemm_act(*args, M, N, K, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE
+
+
 def test_m_zero_is_a_noop():
     # an empty batch launches nothing, so no buffer is needed (shape checks still apply)
     lib = _lib.load()
