@@ -173,6 +173,43 @@ def time_replays(graphs, n: int) -> float:
     return a.elapsed_time(b)
 
 
+def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, reps: int = 20) -> dict:
+    """Qwen3-4B gated MLP block (gate_up 2560x19456 -> silu(gate) * up -> down 9728x2560)
+    at M = 1, 8, 32: the activation fused into the gate_up GEMM's epilogue, against
+    the same GEMMs with the activation as separate torch ops (the reference's
+    GatedMLP.forward: gate_up_proj, silu_and_mul, down_proj).  HIP-graph replay
+    over rotating weight copies."""
+    H, I = 2560, 9728
+    gu = [make_repacked(ops, H, 2 * I, gen, dev) for _ in range(copies)]
+    dn = [make_repacked(ops, I, H, gen, dev) for _ in range(copies)]
+    cg, cd = ops.make_counters(2 * I, dev), ops.make_counters(H, dev)
+    res = {}
+    for M in M_SET:
+        x = torch.randn((M, H), generator=gen, device=dev).to(torch.float16)
+        y = torch.empty((M, 2 * I), dtype=torch.float16, device=dev)
+        h = torch.empty((M, I), dtype=torch.float16, device=dev)
+        o = torch.empty((M, H), dtype=torch.float16, device=dev)
+
+        def unfused(c):
+            ops.gemm(x, gu[c], H, 2 * I, G, counters=cg, out=y)
+            torch.mul(torch.nn.functional.silu(y[:, :I]), y[:, I:], out=h)
+            ops.gemm(h, dn[c], I, H, G, counters=cd, out=o)
+
+        def fused(c):
+            ops.gemm(x, gu[c], H, 2 * I, G, counters=cg, out=h, activation="silu")
+            ops.gemm(h, dn[c], I, H, G, counters=cd, out=o)
+
+        t = {}
+        for name, fn in (("unfused", unfused), ("fused", fused)):
+            g = graph_of(lambda: [fn(c) for c in range(copies)])
+            t[name] = time_replays([g], reps) * 1e3 / (reps * copies)
+        res[str(M)] = {"fused_us": round(t["fused"], 2), "unfused_us": round(t["unfused"], 2),
+                       "speedup": round(t["unfused"] / t["fused"], 3)}
+    return {"workload": "Qwen3-4B gated MLP block: gate_up 2560x19456 + silu(gate)*up + down 9728x2560, int4 group "
+                        "128, fp16; fused = activation in the gate_up GEMM epilogue, unfused = torch silu and mul "
+                        "between the GEMMs", "per_m": res}
+
+
 def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, reps: int = 50) -> dict:
     """Qwen3-30B-A3B-shaped experts: E=128, H=2048, I=768, top-8 of softmax(N(0,1) logits), T=512.
 
@@ -538,6 +575,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the fused/unfused gated MLP block comparison")
     ap.add_argument("--no-stack", action="store_true", help="skip the 70B-shaped stack (35.6 GB of weights)")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the decode step (profiling runs of the other sections; no value is reported)")
@@ -632,6 +670,7 @@ def main() -> int:
                    "peak": MFMA_FP16_PEAK_TFLOPS, "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
                    "kernel": "tiled_kernel", "linears": lin}
 
+    mlp = None if args.no_mlp else mlp_bench(ops, dev, gen)
     moe = None if args.no_moe else moe_bench(ops, dev, gen)
     stack = None if args.no_stack else stack70b_bench(ops, dev, gen)
 
@@ -659,6 +698,7 @@ def main() -> int:
         "decode_kernels": kernels,
         "per_m": per_m,
         "prefill": prefill,
+        "mlp": mlp,
         "moe": moe,
         "stack70b": stack,
         "cpu_baseline": cpu,

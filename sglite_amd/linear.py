@@ -112,6 +112,12 @@ class MergedColumnParallelLinear(_TPLinearBase):
         tp_sizes = [div_even(s, tp_size) for s in output_sizes]
         super().__init__(input_size, sum(output_sizes), input_size, sum(tp_sizes), has_bias, linear_method, tp_size)
 
+    def forward_act(self, x: torch.Tensor, activation: str) -> torch.Tensor:
+        """act(gate) * up of a two-part (gate, up) projection: the layer's forward
+        followed by silu_and_mul / gelu_and_mul (blocks.py:53-55), fused into the
+        GEMM when the linear method has a fused kernel."""
+        return self._linear_method.apply_weights_act(self._weights, x, activation, self.bias)
+
 
 class QKVParallelLinear(_TPLinearBase):
     """Fused q/k/v projection: local N = (Hq/tp + 2 Hkv/tp) * d (linear.py:146-168)."""

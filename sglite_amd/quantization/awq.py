@@ -94,3 +94,9 @@ class AWQLinearMethod(LinearMethodBase):
     def apply_weights(self, weights: Dict[str, Any], x: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
         K = int(weights["_input_size"]) if "_input_size" in weights else int(weights["qweight"].shape[0])
         return cdna4_utils.apply_awq_linear(weights, x, bias, self._group_size(K))
+
+    def apply_weights_act(self, weights: Dict[str, Any], x: torch.Tensor, activation: str,
+                          bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """act(gate) * up in the gate/up GEMM's epilogue (one launch, no [M, N] intermediate)."""
+        K = int(weights["_input_size"]) if "_input_size" in weights else int(weights["qweight"].shape[0])
+        return cdna4_utils.apply_awq_linear(weights, x, bias, self._group_size(K), activation=activation)

@@ -127,3 +127,11 @@ class AWQMarlinLinearMethod(LinearMethodBase):
         if group_size == -1:
             group_size = weights["_input_size"]
         return cdna4_utils.apply_awq_linear(weights, x, bias, group_size)
+
+    def apply_weights_act(self, weights: Dict[str, Any], x: torch.Tensor, activation: str,
+                          bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """act(gate) * up in the gate/up GEMM's epilogue (one launch, no [M, N] intermediate)."""
+        group_size = self.quant_config.group_size
+        if group_size == -1:
+            group_size = weights["_input_size"]
+        return cdna4_utils.apply_awq_linear(weights, x, bias, group_size, activation=activation)

@@ -45,6 +45,22 @@ class LinearMethodBase(ABC):
     def process_weights_after_loading(self, weights: Dict[str, Any]) -> Dict[str, Any]:
         return weights
 
+    def apply_weights_act(self, weights: Dict[str, Any], x: torch.Tensor, activation: str,
+                          bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """act(gate) * up of a merged gate/up projection (gate columns first): the
+        GEMM then silu_and_mul / gelu_and_mul in fp32, as GatedMLP.forward does
+        (blocks.py:51-57, activation.py:11-23).  No counterpart in the reference
+        interface; methods with a fused kernel override it."""
+        y = self.apply_weights(weights, x, bias).float()
+        d = y.shape[-1] // 2
+        if activation == "silu":
+            g = torch.nn.functional.silu(y[..., :d])
+        elif activation == "gelu":
+            g = torch.nn.functional.gelu(y[..., :d])
+        else:
+            raise ValueError(f"Unsupported activation function: {activation}")
+        return (g * y[..., d:]).to(x.dtype)
+
 
 class QuantizationConfig(ABC):
     """Configuration of a quantization scheme (base_config.py:45-91)."""

@@ -139,11 +139,13 @@ def repack_awq_weights(weights: Dict[str, Any], group_size: int) -> Dict[str, An
 
 
 def apply_awq_linear(weights: Dict[str, Any], x: torch.Tensor, bias: Optional[torch.Tensor],
-                     group_size: int) -> torch.Tensor:
+                     group_size: int, activation: Optional[str] = None) -> torch.Tensor:
     """y = x @ W (+ bias) for repacked weights; raw AWQ weights are repacked on the fly.
 
     Output shape x.shape[:-1] + (N,), dtype x.dtype, bias added after the GEMM
-    in the activation dtype (awq.py:133-147; marlin_utils.py:390-415).
+    in the activation dtype (awq.py:133-147; marlin_utils.py:390-415).  With
+    ``activation`` the output is act(gate) * up of the two column halves,
+    x.shape[:-1] + (N / 2,), computed in the GEMM's epilogue.
     """
     if not weights.get("_cdna4", False):
         weights = repack_awq_weights(weights, group_size)
@@ -151,6 +153,7 @@ def apply_awq_linear(weights: Dict[str, Any], x: torch.Tensor, bias: Optional[to
     N = weights["_output_size"]
     G = weights["_group_size"]
     r = ops.Repacked(weights["qweight"], weights["scales"], weights["qzeros"])
-    out_shape = x.shape[:-1] + (N,)
-    y = ops.gemm(x.reshape(-1, x.shape[-1]), r, K, N, G, bias=bias, counters=weights["workspace"])
+    out_shape = x.shape[:-1] + (N if activation is None else N // 2,)
+    y = ops.gemm(x.reshape(-1, x.shape[-1]), r, K, N, G, bias=bias, counters=weights["workspace"],
+                 activation=activation)
     return y.reshape(out_shape)

@@ -117,3 +117,34 @@ def test_fused_equals_unfused_gemm_then_activation(monkeypatch):
     ulp = torch.clamp(ref.abs(), min=2.0 ** -14) * 2.0 ** -10
     assert bool(((fused - ref).abs() <= ulp).all())
     assert (fused == ref).float().mean().item() > 0.99
+
+
+@pytest.mark.parametrize("method_name", ["awq", "awq_marlin"])
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_gated_mlp_block_against_oracle(method_name, act):
+    """GatedMLP (blocks.py:27-57) on the AWQ plugin: gate_up with the activation
+    fused, then down; oracle: GEMM, silu_and_mul / gelu_and_mul rounded, GEMM."""
+    from sglite_amd.mlp import GatedMLP
+    from sglite_amd.quantization import get_quantization_config
+
+    torch.set_default_dtype(torch.float16)
+    try:
+        cfg = get_quantization_config(method_name).from_config(
+            {"quant_method": "awq", "bits": 4, "group_size": 128, "zero_point": True})
+        H, I = 512, 768
+        mlp = GatedMLP(H, I, act, linear_method=cfg.get_linear_method())
+        tgu = oracle.make_awq_linear(H, 2 * I, 128, seed=21)
+        tdn = oracle.make_awq_linear(I, H, 128, seed=22)
+        sd = {f"mlp.gate_up_proj.{k}": v.to(DEV) for k, v in tgu.items()}
+        sd.update({f"mlp.down_proj.{k}": v.to(DEV) for k, v in tdn.items()})
+        assert sorted(mlp.state_dict_keys("mlp")) == sorted(sd)
+        mlp.load_state_dict(sd, prefix="mlp")
+        for M in (1, 7, 40):
+            x = oracle.make_activation(M, H, seed=30 + M)
+            y = mlp(x.to(DEV))
+            h = _reference(x, tgu, 128, None, act)
+            ref = oracle.awq_gemm(h, tdn["qweight"], tdn["qzeros"], tdn["scales"], None, 128)
+            ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+            assert ok, (method_name, act, M, err, mx)
+    finally:
+        torch.set_default_dtype(torch.float32)
