@@ -83,16 +83,17 @@ def test_every_two_tile_gemv_shape(variant, M, monkeypatch):
 
 @pytest.mark.parametrize("variant", [20202, 20401, 20204])
 @pytest.mark.parametrize("M", [3, 20])
-def test_every_two_tile_decode_shape(variant, M, monkeypatch):
-    _check(M, 4096, 1040, env={"SGL_AWQ_SKINNY_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 0}, kernel="skinny_kernel",
-           monkeypatch=monkeypatch)
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_every_two_tile_decode_shape(variant, M, G, monkeypatch):
+    _check(M, 4096, 1040, G=G, env={"SGL_AWQ_SKINNY_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 0},
+           kernel="skinny_kernel", monkeypatch=monkeypatch)
 
 
 @pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("ks", [1, 3])
-@pytest.mark.parametrize("G", [64, 128, -1])
+@pytest.mark.parametrize("G", [32, 64, 128, -1])
 def test_every_prefill_row_block(bm, ks, G, monkeypatch):
-    K = 1280 if G != -1 else 1152
+    K = 1312 if G == 32 else (1280 if G != -1 else 1152)
     _check(70, K, 1040, G=G, env={"SGL_AWQ_TILED_BM": bm, "SGL_AWQ_TILED_KS": ks, "SGL_AWQ_TILED_MIN_M": 1},
            kernel="tiled_kernel", monkeypatch=monkeypatch)
 
