@@ -1,11 +1,13 @@
 // W4A16 GEMM planning and dispatch for gfx950: out[M, N] = x[M, K] @ W
-// (+ bias), fp32 accumulation.  Three kernels share the CDNA4 tile layout
-// (awq_device.h):
+// (+ bias), fp32 accumulation, optionally with the gated activation of a
+// merged gate/up projection fused (out[M, N / 2] = act(gate) * up).  Three
+// kernels share the CDNA4 tile layout (awq_device.h):
 //
 //  * gemv_kernel (awq_gemv.hip): batches of a few rows, HBM-bound;
 //  * skinny_kernel (awq_skinny.hip): decode batches up to 32 rows, HBM-bound
 //    split-K;
-//  * tiled_kernel (awq_tiled.hip): prefill, MFMA-bound.
+//  * tiled_kernel (awq_tiled.hip): prefill (MFMA-bound) and 16-32 rows on
+//    large matrices, split K through a second reduction kernel.
 //
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)

@@ -1,4 +1,5 @@
-// Prefill W4A16 GEMM (M > 32): MFMA-bound tiled kernel for gfx950.
+// Tiled W4A16 GEMM for gfx950: prefill batches (MFMA-bound at M >= ~256), and
+// batches of 16-32 rows on wide or deep matrices (32-row block, split K).
 //
 // A workgroup of 4 waves computes BM x 256 outputs; wave w owns the 64 output
 // columns of four 16-column weight tiles and all BM rows, so every packed
@@ -440,9 +441,11 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
 // activation offsets (bm rows of K elements) stay below 2^31 bytes.
 int64_t tiled_max_k(int bm) { return ((int64_t(1) << 31) - 1) / (2 * (int64_t)bm); }
 
+// (The split K of this kernel reduces in a second kernel, so it needs no
+// arrival counters; `counters` is accepted for the common launch signature.)
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
-                        hipStream_t s) {
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* /*counters*/,
+                        int act, hipStream_t s) {
   if (p.grid_x * p.grid_y * p.ks >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
   TiledArgs a;
   a.x = x;
