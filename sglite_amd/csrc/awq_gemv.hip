@@ -374,6 +374,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
 #define SGL_GEMV_M(NTW_, WN_, WK_, KPW_) SGL_GEMV_X(NTW_, WN_, WK_, KPW_, 1) SGL_GEMV_X(NTW_, WN_, WK_, KPW_, 2)
   SGL_GEMV_M(1, 1, 4, 8)
   SGL_GEMV_M(1, 1, 8, 4)
+  SGL_GEMV_M(1, 1, 8, 3)
   SGL_GEMV_M(2, 1, 4, 4)
   SGL_GEMV_M(2, 1, 8, 4)
   SGL_GEMV_M(2, 2, 2, 8)
@@ -392,7 +393,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
 // Variant code: ntw * 10000 + wn * 1000 + wk * 10 + kpw.
 bool gemv_variant_ok(int v) {
   switch (v) {
-    case 11048: case 11084: case 21044: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
+    case 11048: case 11083: case 11084: case 21044: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
       return true;
     default:
       return false;
