@@ -46,34 +46,68 @@ bool skinny_variant_ok(int v) {
   }
 }
 
+// Split of K for a GEMV variant: the smallest count that keeps each wave
+// within its KPW k-tiles and the workgroup's activation slice within 8 loads
+// per thread and 60 KiB of LDS (two workgroups per CU).  0 if none fits.
+struct GemvSplit {
+  int64_t ks, ktc, xpt, lds;
+};
+GemvSplit gemv_split(const Geom& g, int v, int64_t ks) {
+  const int ntw = v / 10000, wn = (v / 1000) % 10, wk = (v / 10) % 100, kpw = v % 10;
+  const int64_t mt = (g.M + 15) / 16, threads = 64 * wn * wk;
+  for (ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT)); ks <= g.KT; ++ks) {
+    const int64_t ktc = (g.KT + ks - 1) / ks;
+    const int64_t xpt = (g.M * ktc * 16 + threads - 1) / threads;
+    const int64_t lds = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * wn * mt * ntw * 1024);
+    if ((ktc + wk - 1) / wk <= kpw && xpt <= 8 && lds <= 61440) return {(g.KT + ktc - 1) / ktc, ktc, xpt, lds};
+  }
+  return {0, 0, 0, 0};
+}
+int64_t gemv_min_ks(const Geom& g, int v) {
+  const int wk = (v / 10) % 100, kpw = v % 10;
+  return (g.KT + (int64_t)wk * kpw - 1) / ((int64_t)wk * kpw);
+}
 }  // namespace
 
-// GEMV plan (small M, one quantisation group per 128-row tile): every wave
-// issues the loads of all its k-tiles at once.  Variant code
-// ntw * 10000 + wn * 1000 + wk * 10 + kpw.  The rules come from a sweep of the
-// variants and splits over the Qwen3-4B and Llama-3-8B decode shapes on
-// MI355X; the split-K is the smallest that keeps each wave within its k-tile
-// budget and the workgroup's activation slice within 8 loads per thread and
-// 64 KiB of LDS.
-// Where the GEMV kernel wins (same sweep): M <= 4, and M <= 8 on K <= 3072;
-// at larger M the per-workgroup activation slice costs more than the wider
-// decode kernel's per-wave fragments.
-bool gemv_preferred(const Geom& g) {
-  const int forced = env_int("SGL_AWQ_GEMV_MAX_M", -1);
-  if (forced >= 0) return g.M <= forced;
-  return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
-}
-
-// 8 waves, one column tile per workgroup, at most 4 k-tiles per wave -- 3 when
-// the whole K fits in 24 k-tiles, so that fewer load slots re-read a wave's
-// last tile (3-6% faster on 20-k-tile layers at M = 1 and 8; a 3-slot shape
-// would split K beyond 24 k-tiles).  With a fused gate/up activation a
-// workgroup holds one gate tile and its up tile: 4 waves at up to 4 rows, 8
-// waves at 5-8 rows (graph-replay sweep of the two-tile shapes over the
-// Qwen3-4B and Llama-3-8B gate_up projections).
+// GEMV variant (code ntw * 10000 + wn * 1000 + wk * 10 + kpw): 8 waves of at
+// most 3 or 4 k-tiles each, whichever splits K fewer times (3 on a tie: fewer
+// load slots re-read a wave's last tile).  One column tile per workgroup up
+// to 4 rows; from 5 rows (7 on layers of >= 1024 column tiles, where the
+// workgroup count matters more) two column tiles share a workgroup of 16
+// waves, which halves the activation slices staged per weight byte.  With a
+// fused gate/up activation a workgroup holds one gate tile and its up tile:
+// 4 waves at up to 4 rows, 8 waves at 5-8 rows.  (Graph-replay sweep of the
+// variants over the Qwen3-4B, Llama-3-8B and Llama-3-70B shapes.)
 int gemv_default_variant(const Geom& g, int act) {
   if (act) return g.M <= 4 ? 21044 : 21084;
-  return g.KT <= 24 ? 11083 : 11084;
+  const int wn = g.M >= (g.NT >= 1024 ? 7 : 5) ? 2 : 1;
+  const int v3 = 10083 + wn * 1000, v4 = v3 + 1;
+  const int64_t k3 = gemv_split(g, v3, gemv_min_ks(g, v3)).ks, k4 = gemv_split(g, v4, gemv_min_ks(g, v4)).ks;
+  return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? v3 : v4;
+}
+
+// Where the GEMV kernel wins over the decode (skinny) kernel, from a
+// graph-replay sweep of M = 1..8 over the Qwen3-4B, Llama-3-8B and
+// Llama-3-70B projections on MI355X:
+//  * up to 4 rows, except 3-4 rows on very wide layers (>= 2048 column
+//    tiles: 5-10% slower than the skinny kernel's two-tile waves);
+//  * 5-8 rows, except on wide layers (>= 1024 column tiles) with K beyond 24
+//    k-tiles, narrow ones (< 384 column tiles) with K of 25-63 k-tiles, and
+//    wherever the 60 KiB activation slice would cut a workgroup's K range to
+//    16 k-tiles or fewer (2 per wave): there the workgroup's staged
+//    activation slice costs more than the skinny kernel's per-wave fragments.
+// A fused gate/up activation keeps the GEMV kernel up to 4 rows, and up to 8
+// rows when K fits in 24 k-tiles.
+bool gemv_preferred(const Geom& g, int act) {
+  const int forced = env_int("SGL_AWQ_GEMV_MAX_M", -1);
+  if (forced >= 0) return g.M <= forced;
+  if (act) return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
+  if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
+  if (g.M > 8) return false;
+  if (g.KT <= 24) return true;
+  if (g.NT >= 1024 || (g.NT < 384 && g.KT < 64)) return false;
+  const int v = gemv_default_variant(g, 0);
+  return gemv_split(g, v, gemv_min_ks(g, v)).ktc > 16;
 }
 
 bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
@@ -82,33 +116,20 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
   const int env = env_int("SGL_AWQ_GEMV_VARIANT", 0);
   if (gemv_variant_ok(env) && (!act || env / 10000 == 2)) v = env;
   if (!gemv_variant_ok(v)) return false;
-  const int ntw = v / 10000, wn = (v / 1000) % 10, wk = (v / 10) % 100, kpw = v % 10;
-  const int64_t mt = (g.M + 15) / 16, threads = 64 * wn * wk;
-  const int64_t gx = (g.NT + (int64_t)wn * ntw - 1) / ((int64_t)wn * ntw);
-  int64_t ks = std::max<int64_t>(1, (g.KT + (int64_t)wk * kpw - 1) / ((int64_t)wk * kpw));
+  const int ntw = v / 10000, wn = (v / 1000) % 10;
   const int env_ks = env_int("SGL_AWQ_GEMV_KS", 0);
-  if (env_ks > 0) ks = env_ks;
-  for (;;) {
-    ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
-    const int64_t ktc = (g.KT + ks - 1) / ks;
-    const int64_t xpt = (g.M * ktc * 16 + threads - 1) / threads;
-    const int64_t lds = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * wn * mt * ntw * 1024);
-    if ((ktc + wk - 1) / wk > kpw || xpt > 8 || lds > 61440) {
-      if (ks >= g.KT) return false;
-      ks *= 2;
-      continue;
-    }
-    p.kind = 2;
-    p.variant = v;
-    p.ktc = (int)ktc;
-    p.ks = (int)((g.KT + ktc - 1) / ktc);
-    p.xpt = xpt <= 1 ? 1 : (xpt <= 2 ? 2 : (xpt <= 4 ? 4 : 8));
-    p.grid_x = gx;
-    p.grid_y = p.ks;
-    p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
-    p.lds_bytes = lds;
-    return true;
-  }
+  const GemvSplit sp = gemv_split(g, v, env_ks > 0 ? env_ks : gemv_min_ks(g, v));
+  if (sp.ks == 0) return false;
+  p.kind = 2;
+  p.variant = v;
+  p.ktc = (int)sp.ktc;
+  p.ks = (int)sp.ks;
+  p.xpt = sp.xpt <= 1 ? 1 : (sp.xpt <= 2 ? 2 : (sp.xpt <= 4 ? 4 : 8));
+  p.grid_x = (g.NT + (int64_t)wn * ntw - 1) / ((int64_t)wn * ntw);
+  p.grid_y = p.ks;
+  p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
+  p.lds_bytes = sp.lds;
+  return true;
 }
 
 // Batches of 16..32 rows: the tiled kernel (32-row block, split K) beats the
@@ -129,7 +150,7 @@ bool tiled_preferred(const Geom& g) {
 GemmPlan plan_gemm(const Geom& g, int act) {
   GemmPlan p{};
   const bool tiled = tiled_preferred(g);
-  if (!tiled && gemv_preferred(g) && plan_gemv(g, p, act)) return p;
+  if (!tiled && gemv_preferred(g, act) && plan_gemv(g, p, act)) return p;
   if (!tiled) {
     p.kind = 0;
     // Variant code: ntw * 10000 + wn * 100 + wk.  Chosen from a sweep of all

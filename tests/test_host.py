@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import awq_oracle as oracle
-from sglite_amd import _lib
+from sglite_amd import _lib, ops
 from sglite_amd.quantization import (LinearMethodBase, QuantizationConfig, UnquantizedLinearMethod,
                                      get_quantization_config, set_weight_attrs)
 
@@ -76,6 +76,23 @@ def test_workspace_query_is_bounded():
             ks, rem = divmod(ws, M * NT * 16 * 4)
             assert rem == 0 and (ks == 0 or 2 <= ks <= 16)
     assert lib.awq_workspace_bytes(8192, 28672, 4096, 128) == 0  # full grids never split
+
+
+@pytest.mark.parametrize("K,N,routes", [
+    (2560, 6144, "gggggggg"),    # Qwen3-4B qkv: short K, GEMV throughout
+    (4096, 2560, "ggggssss"),    # Qwen3-4B o_proj: narrow, 32 k-tiles
+    (2560, 19456, "gggggggg"),   # Qwen3-4B gate_up
+    (9728, 2560, "gggggggg"),    # Qwen3-4B down: K splits keep 26 k-tiles per workgroup
+    (4096, 6144, "gggggggs"),    # Llama-3-8B qkv: at 8 rows the activation slice halves the K range
+    (4096, 28672, "ggggssss"),   # Llama-3-8B gate_up: wide
+    (8192, 57344, "ggssssss"),   # Llama-3-70B gate_up: very wide
+    (28672, 8192, "gggggggg"),   # Llama-3-70B down
+])
+def test_decode_routing(K, N, routes):
+    """Kernel choice for 1..8 rows (g = GEMV, s = skinny decode kernel)."""
+    for M, r in enumerate(routes, start=1):
+        want = {"g": "gemv_kernel", "s": "skinny_kernel"}[r]
+        assert ops.gemm_kernel(M, N, K, 128) == want, (M, K, N)
 
 
 @pytest.mark.parametrize("K,N,G,dtype,msg", [
