@@ -119,10 +119,12 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
  * gelu_and_mul of layers/activation.py:11-23) without the [M, N]
  * intermediate or its second launch.  N % 32 == 0; out 8-byte aligned.
  * Workspace and counters as for awq_w4a16_gemm, sized by
- * awq_workspace_bytes_act (no counterpart in the reference: a fusion of
- * two of its calls). */
+ * awq_workspace_bytes_act; awq_gemm_kernel_kind_act names the kernel it runs
+ * (codes as for awq_gemm_kernel_kind).  No counterpart in the reference: a
+ * fusion of two of its calls. */
 enum { AWQ_ACT_SILU = 1, AWQ_ACT_GELU = 2 };
 int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G);
+int awq_gemm_kernel_kind_act(int64_t M, int64_t N, int64_t K, int64_t G);
 int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
                        int64_t ws_bytes, int32_t* counters, awq_stream_t stream);

@@ -43,6 +43,7 @@ SIGNATURES = {
     "awq_gemm_kernel_kind": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp]),
     "awq_workspace_bytes_act": (_i64, [_i64, _i64, _i64, _i64]),
+    "awq_gemm_kernel_kind_act": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm_act": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp,
                                   _vp]),
     "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),

@@ -216,6 +216,16 @@ int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G) {
   return plan_gemm(make_geom(M, N, K, Gr), kActSilu).ws_bytes;
 }
 
+int awq_gemm_kernel_kind_act(int64_t M, int64_t N, int64_t K, int64_t G) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be positive");
+  if (N % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "a gate/up projection needs N %% 32 == 0, got %lld", (long long)N);
+  return plan_gemm(make_geom(M, N, K, Gr), kActSilu).kind;
+}
+
 int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
                        int64_t ws_bytes, int32_t* counters, awq_stream_t stream) {

@@ -46,9 +46,13 @@ bool skinny_variant_ok(int v) {
   }
 }
 
+// LDS a GEMV workgroup may use for its activation slice: gfx950 gives one
+// workgroup up to 160 KiB; 4 KiB stay free for the kernel's static LDS.
+constexpr int64_t kGemvLdsMax = 156 * 1024;
+
 // Split of K for a GEMV variant: the smallest count that keeps each wave
 // within its KPW k-tiles and the workgroup's activation slice within 8 loads
-// per thread and 60 KiB of LDS (two workgroups per CU).  0 if none fits.
+// per thread and kGemvLdsMax of LDS.  0 if none fits.
 struct GemvSplit {
   int64_t ks, ktc, xpt, lds;
 };
@@ -59,7 +63,7 @@ GemvSplit gemv_split(const Geom& g, int v, int64_t ks) {
     const int64_t ktc = (g.KT + ks - 1) / ks;
     const int64_t xpt = (g.M * ktc * 16 + threads - 1) / threads;
     const int64_t lds = std::max<int64_t>(g.M * (ktc * 128 + 8) * 2, (int64_t)wk * wn * mt * ntw * 1024);
-    if ((ktc + wk - 1) / wk <= kpw && xpt <= 8 && lds <= 61440) return {(g.KT + ktc - 1) / ktc, ktc, xpt, lds};
+    if ((ktc + wk - 1) / wk <= kpw && xpt <= 8 && lds <= kGemvLdsMax) return {(g.KT + ktc - 1) / ktc, ktc, xpt, lds};
   }
   return {0, 0, 0, 0};
 }
@@ -87,15 +91,15 @@ int gemv_default_variant(const Geom& g, int act) {
 }
 
 // Where the GEMV kernel wins over the decode (skinny) kernel, from a
-// graph-replay sweep of M = 1..8 over the Qwen3-4B, Llama-3-8B and
+// graph-replay sweep of M = 1..16 over the Qwen3-4B, Llama-3-8B and
 // Llama-3-70B projections on MI355X:
 //  * up to 4 rows, except 3-4 rows on very wide layers (>= 2048 column
 //    tiles: 5-10% slower than the skinny kernel's two-tile waves);
-//  * 5-8 rows, except on wide layers (>= 1024 column tiles) with K beyond 24
-//    k-tiles, narrow ones (< 384 column tiles) with K of 25-63 k-tiles, and
-//    wherever the 60 KiB activation slice would cut a workgroup's K range to
-//    16 k-tiles or fewer (2 per wave): there the workgroup's staged
-//    activation slice costs more than the skinny kernel's per-wave fragments.
+//  * 5-16 rows, except on wide layers (>= 1024 column tiles) with K beyond
+//    24 k-tiles, narrow ones (< 384 column tiles) with K of 25-63 k-tiles, and
+//    wherever the activation slice would cut a workgroup's K range to 16
+//    k-tiles or fewer (2 per wave): there the workgroup's staged activation
+//    slice costs more than the skinny kernel's per-wave fragments.
 // A fused gate/up activation keeps the GEMV kernel up to 4 rows, and up to 8
 // rows when K fits in 24 k-tiles.
 bool gemv_preferred(const Geom& g, int act) {
@@ -103,7 +107,7 @@ bool gemv_preferred(const Geom& g, int act) {
   if (forced >= 0) return g.M <= forced;
   if (act) return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
   if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
-  if (g.M > 8) return false;
+  if (g.M > 16) return false;
   if (g.KT <= 24) return true;
   if (g.NT >= 1024 || (g.NT < 384 && g.KT < 64)) return false;
   const int v = gemv_default_variant(g, 0);
@@ -132,24 +136,34 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
   return true;
 }
 
-// Batches of 16..32 rows: the tiled kernel (32-row block, split K) beats the
-// decode kernel on wide or deep matrices (graph replay of the Qwen3-4B and
-// Llama-3-8B linears at M = 16, 24, 32 on MI355X: at M = 32 qkv, gate_up and
-// down run 8-15% faster, e.g. 29.1 -> 24.7 us for a 4096 x 28672 gate_up;
-// the o_proj shapes stay 8-15% faster on the decode kernel); at M = 16 only
-// gate_up-sized matrices gain.
-bool tiled_preferred(const Geom& g) {
+// Batches of 6..32 rows: the tiled kernel (32-row block, K split up to 16
+// ways) beats both decode kernels on deep or wide matrices (graph replay of
+// the Qwen3-4B, Llama-3-8B and Llama-3-70B linears at M = 5..32 on MI355X):
+//  * 17-32 rows: K * N >= 12M with N >= 6144 or K >= 8192 (at M = 32 qkv,
+//    gate_up and down run 8-15% faster, e.g. 29.1 -> 24.7 us for a
+//    4096 x 28672 gate_up; the o_proj shapes stay 8-15% faster on the decode
+//    kernel);
+//  * 10-16 rows: K >= 8192 and K * N >= 40M (14336 x 4096 down: 19.4 ->
+//    15.4 us at M = 16; 28672 x 8192 down: 67.7 -> 37.3 us);
+//  * 6-9 rows: K >= 8192 and 8192 <= N < 32768 (the 70B qkv, o and down
+//    projections: 48.7 -> 36.4 us for the down projection at M = 8);
+//  * 14-16 rows on gate_up-sized matrices (N >= 16384, K * N >= 20M).
+// A fused gate/up activation uses the 17-32 and 14-16 row rules only.
+bool tiled_preferred(const Geom& g, int act) {
   const int forced = env_int("SGL_AWQ_TILED_MIN_M", 0);
   if (forced > 0) return g.M >= forced;
   if (g.M > 32) return true;
   const int64_t kn = g.K * g.N;
   if (g.M > 16) return kn >= 12000000 && (g.N >= 6144 || g.K >= 8192);
-  return g.M == 16 && g.N >= 16384 && kn >= 20000000;
+  if (g.M >= 14 && g.N >= 16384 && kn >= 20000000) return true;
+  if (act) return false;
+  if (g.M >= 10) return g.K >= 8192 && kn >= 40000000;
+  return g.M >= 6 && g.K >= 8192 && g.N >= 8192 && g.N < 32768;
 }
 
 GemmPlan plan_gemm(const Geom& g, int act) {
   GemmPlan p{};
-  const bool tiled = tiled_preferred(g);
+  const bool tiled = tiled_preferred(g, act);
   if (!tiled && gemv_preferred(g, act) && plan_gemv(g, p, act)) return p;
   if (!tiled) {
     p.kind = 0;

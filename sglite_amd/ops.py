@@ -150,10 +150,14 @@ def workspace_bytes(M: int, N: int, K: int, group_size: int) -> int:
 KERNEL_NAMES = {0: "skinny_kernel", 1: "tiled_kernel", 2: "gemv_kernel"}
 
 
-def gemm_kernel(M: int, N: int, K: int, group_size: int) -> str:
-    """Name of the kernel ``gemm`` runs for this shape."""
+def gemm_kernel(M: int, N: int, K: int, group_size: int, activation: Optional[str] = None) -> str:
+    """Name of the kernel ``gemm`` runs for this shape (with ``activation``:
+    the fused gate/up GEMM's kernel)."""
     G = resolve_group_size(group_size, K)
-    return KERNEL_NAMES[_lib.check(_lib.load().awq_gemm_kernel_kind(M, N, K, G), "awq_gemm_kernel_kind")]
+    lib = _lib.load()
+    if activation is None:
+        return KERNEL_NAMES[_lib.check(lib.awq_gemm_kernel_kind(M, N, K, G), "awq_gemm_kernel_kind")]
+    return KERNEL_NAMES[_lib.check(lib.awq_gemm_kernel_kind_act(M, N, K, G), "awq_gemm_kernel_kind_act")]
 
 
 def make_counters(N: int, device: torch.device) -> torch.Tensor:

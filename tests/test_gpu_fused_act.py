@@ -41,7 +41,7 @@ def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env
     for k, v in (env or {}).items():
         monkeypatch.setenv(k, str(v))
     if kernel is not None:
-        assert ops.gemm_kernel(M, N, K, G) == kernel
+        assert ops.gemm_kernel(M, N, K, G, activation=act) == kernel
     cnt = ops.make_counters(N, DEV)
     x = oracle.make_activation(M, K, seed=seed + 3, dtype=dtype)
     y = ops.gemm(x.to(DEV), r, K, N, G, bias=None if bias is None else bias.to(DEV), counters=cnt, activation=act)

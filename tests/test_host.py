@@ -79,20 +79,34 @@ def test_workspace_query_is_bounded():
 
 
 @pytest.mark.parametrize("K,N,routes", [
-    (2560, 6144, "gggggggg"),    # Qwen3-4B qkv: short K, GEMV throughout
-    (4096, 2560, "ggggssss"),    # Qwen3-4B o_proj: narrow, 32 k-tiles
-    (2560, 19456, "gggggggg"),   # Qwen3-4B gate_up
-    (9728, 2560, "gggggggg"),    # Qwen3-4B down: K splits keep 26 k-tiles per workgroup
-    (4096, 6144, "gggggggs"),    # Llama-3-8B qkv: at 8 rows the activation slice halves the K range
-    (4096, 28672, "ggggssss"),   # Llama-3-8B gate_up: wide
-    (8192, 57344, "ggssssss"),   # Llama-3-70B gate_up: very wide
-    (28672, 8192, "gggggggg"),   # Llama-3-70B down
+    (2560, 6144, "g" * 16),                    # Qwen3-4B qkv: short K, GEMV throughout
+    (4096, 2560, "g" * 4 + "s" * 12),          # Qwen3-4B o_proj: narrow, 32 k-tiles
+    (2560, 19456, "g" * 13 + "t" * 3),         # Qwen3-4B gate_up
+    (9728, 2560, "g" * 16),                    # Qwen3-4B down: split K keeps 26 k-tiles per workgroup
+    (4096, 6144, "g" * 16),                    # Llama-3-8B qkv
+    (4096, 28672, "g" * 4 + "s" * 9 + "t" * 3),  # Llama-3-8B gate_up: wide
+    (14336, 4096, "g" * 9 + "t" * 7),          # Llama-3-8B down: deep
+    (8192, 10240, "g" * 5 + "t" * 11),         # Llama-3-70B qkv
+    (8192, 57344, "gg" + "s" * 7 + "t" * 7),   # Llama-3-70B gate_up: very wide
+    (28672, 8192, "g" * 5 + "t" * 11),         # Llama-3-70B down
 ])
 def test_decode_routing(K, N, routes):
-    """Kernel choice for 1..8 rows (g = GEMV, s = skinny decode kernel)."""
-    for M, r in enumerate(routes, start=1):
-        want = {"g": "gemv_kernel", "s": "skinny_kernel"}[r]
-        assert ops.gemm_kernel(M, N, K, 128) == want, (M, K, N)
+    """Kernel choice for 1..16 rows (g = GEMV, s = skinny decode kernel, t = tiled)."""
+    names = {"g": "gemv_kernel", "s": "skinny_kernel", "t": "tiled_kernel"}
+    got = "".join(next(k for k, v in names.items() if v == ops.gemm_kernel(M, N, K, 128))
+                  for M in range(1, len(routes) + 1))
+    assert got == routes, (K, N)
+
+
+def test_fused_activation_routing():
+    """The fused gate/up GEMM keeps the GEMV kernel to 8 rows on short K and the
+    skinny kernel beyond, while the plain GEMM takes the GEMV kernel to 16 rows."""
+    assert ops.gemm_kernel(12, 2080, 2048, 128) == "gemv_kernel"
+    assert ops.gemm_kernel(12, 2080, 2048, 128, activation="silu") == "skinny_kernel"
+    assert ops.gemm_kernel(8, 19456, 2560, 128, activation="silu") == "gemv_kernel"
+    assert ops.gemm_kernel(300, 1056, 1024, 128, activation="gelu") == "tiled_kernel"
+    with pytest.raises(ValueError, match="N % 32"):
+        ops.gemm_kernel(1, 2064, 1024, 128, activation="silu")
 
 
 @pytest.mark.parametrize("K,N,G,dtype,msg", [
