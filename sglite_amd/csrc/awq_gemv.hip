@@ -377,6 +377,11 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   SGL_GEMV_M(1, 1, 8, 3)
   SGL_GEMV_M(1, 2, 8, 3)
   SGL_GEMV_M(1, 2, 8, 4)
+  SGL_GEMV_M(1, 1, 8, 6)
+  SGL_GEMV_M(1, 1, 8, 8)
+  SGL_GEMV_M(1, 1, 16, 5)
+  SGL_GEMV_M(1, 1, 16, 6)
+  SGL_GEMV_M(1, 1, 16, 8)
   SGL_GEMV_M(2, 1, 4, 4)
   SGL_GEMV_M(2, 1, 8, 4)
   SGL_GEMV_M(2, 2, 2, 8)
@@ -395,7 +400,8 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
 // Variant code: ntw * 10000 + wn * 1000 + wk * 10 + kpw.
 bool gemv_variant_ok(int v) {
   switch (v) {
-    case 11048: case 11083: case 11084: case 12083: case 12084: case 21044: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
+    case 11048: case 11083: case 11084: case 11086: case 11088: case 11165: case 11166: case 11168: case 12083:
+    case 12084: case 21044: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
       return true;
     default:
       return false;

@@ -153,7 +153,7 @@ def test_gemm_golden_fixtures():
 
 def test_split_k_is_deterministic():
     ops = _ops()
-    K, N, G = 8192, 512, 128  # few column tiles: the plan splits K across workgroups
+    K, N, G = 28672, 512, 128  # few column tiles, 224 k-tiles: the plan splits K across workgroups
     _, d = _linear(K, N, G, seed=500)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
@@ -330,8 +330,8 @@ def test_decode_bf16_variants(M, monkeypatch):
         assert ok, (variant, err, mx)
 
 
-@pytest.mark.parametrize("variant", [11048, 11083, 11084, 12083, 12084, 21044, 21084, 22028, 22044, 24024, 24042,
-                                     14044])
+@pytest.mark.parametrize("variant", [11048, 11083, 11084, 11086, 11088, 11165, 11166, 11168, 12083, 12084, 21044,
+                                     21084, 22028, 22044, 24024, 24042, 14044])
 @pytest.mark.parametrize("G", [128, -1])
 def test_every_gemv_variant(variant, G, monkeypatch):
     """Each small-batch GEMV instantiation, with and without cross-workgroup
@@ -353,6 +353,25 @@ def test_every_gemv_variant(variant, G, monkeypatch):
             ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
             assert ok, (variant, G, ks, M, err, mx)
         assert int(cnt.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("K,N", [(4224, 136), (6144, 200), (8192, 72), (9728, 160), (11008, 88), (14336, 96)])
+def test_gemv_unsplit_deep_k(K, N):
+    """One and two rows over K of 33-112 k-tiles: the default plan covers the
+    whole K in one workgroup of 8 or 16 waves of up to 8 k-tiles each."""
+    ops = _ops()
+    G = 128
+    t, d = _linear(K, N, G, seed=K % 1009 + N)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    cnt = ops.make_counters(N, DEV)
+    for M in (1, 2):
+        assert ops.gemm_kernel(M, N, K, G) == "gemv_kernel"
+        assert ops.workspace_bytes(M, N, K, G) == 0  # no split K
+        x = oracle.make_activation(M, K, seed=M + 5)
+        y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
+        ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
+        ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+        assert ok, (K, N, M, err, mx)
 
 
 @pytest.mark.parametrize("M", [1, 4])

@@ -98,6 +98,17 @@ def test_decode_routing(K, N, routes):
     assert got == routes, (K, N)
 
 
+def test_gemv_keeps_deep_k_unsplit_at_one_or_two_rows():
+    """Up to 128 k-tiles one GEMV workgroup covers K at 1-2 rows (no split-K
+    workspace); from 4 rows the 8-wave plan splits K again."""
+    for K in (4224, 6144, 8192, 9728, 11008, 14336):
+        for M in (1, 2):
+            assert ops.gemm_kernel(M, 4096, K, 128) == "gemv_kernel"
+            assert ops.workspace_bytes(M, 4096, K, 128) == 0, (M, K)
+    assert ops.workspace_bytes(4, 2560, 9728, 128) > 0
+    assert ops.workspace_bytes(1, 8192, 28672, 128) > 0  # 224 k-tiles still split
+
+
 def test_fused_activation_routing():
     """The fused gate/up GEMM keeps the GEMV kernel to 8 rows on short K and the
     skinny kernel beyond, while the plain GEMM takes the GEMV kernel to 16 rows."""
@@ -140,7 +151,7 @@ def test_null_and_misaligned_pointers_rejected():
 def test_missing_workspace_is_reported_before_launch():
     lib = _lib.load()
     fake = 0x10000
-    K, N, M = 8192, 512, 1  # 32 column tiles: the plan splits K across workgroups
+    K, N, M = 28672, 512, 1  # 32 column tiles, 224 k-tiles: the plan splits K across workgroups
     need = lib.awq_workspace_bytes(M, N, K, 128)
     assert need > 0
     st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, None, 0, None, None)
