@@ -75,13 +75,14 @@ int64_t gemv_min_ks(const Geom& g, int v) {
 
 // GEMV variant (code ntw * 10000 + wn * 1000 + wk * 10 + kpw): 8 waves of at
 // most 3 or 4 k-tiles each, whichever splits K fewer times (3 on a tie: fewer
-// load slots re-read a wave's last tile).  At 1-2 rows a K of 25-128 k-tiles
-// goes to the smallest of 8 waves x 4, 6 or 8 and 16 waves x 5, 6 or 8
-// k-tiles that covers it: a split costs a cross-workgroup handoff (~1.7 us),
-// more than the workgroups it adds save (Qwen3-4B down 8.4 -> 7.5 us,
-// Llama-3-8B down 12.2 -> 11.0 us, 70B-sized o 12.5 -> 10.9 us at M = 1; at
-// 4 rows the larger activation slices lose).  One column tile per workgroup up
-// to 4 rows; from 5 rows (7 on layers of >= 1024 column tiles, where the
+// load slots re-read a wave's last tile).  At 1-3 rows a K of 25-128 k-tiles
+// (up to 6 rows for 65-80 k-tiles) goes to the smallest of 8 waves x 4, 6 or
+// 8 and 16 waves x 5, 6 or 8 k-tiles that covers it: a split costs a
+// cross-workgroup handoff (~1.7 us), more than the workgroups it adds save
+// (Qwen3-4B down 8.4 -> 7.5 us at M = 1, 9.9 -> 9.3 us at M = 6; Llama-3-8B
+// down 12.2 -> 11.0 us and 70B-sized o 12.5 -> 10.9 us at M = 1; at 4 rows
+// and more on other depths the larger activation slices lose).  One column
+// tile per workgroup up to 4 rows; from 5 rows (7 on layers of >= 1024 column tiles, where the
 // workgroup count matters more) two column tiles share a workgroup of 16
 // waves, which halves the activation slices staged per weight byte.  With a
 // fused gate/up activation a workgroup holds one gate tile and its up tile:
@@ -89,7 +90,7 @@ int64_t gemv_min_ks(const Geom& g, int v) {
 // variants over the Qwen3-4B, Llama-3-8B and Llama-3-70B shapes.)
 int gemv_default_variant(const Geom& g, int act) {
   if (act) return g.M <= 4 ? 21044 : 21084;
-  if (g.M <= 2 && g.KT > 24 && g.KT <= 128) {
+  if (g.KT > 24 && g.KT <= 128 && (g.M <= 3 || (g.M <= 6 && g.KT > 64 && g.KT <= 80))) {
     for (int v : {11084, 11086, 11088, 11165, 11166, 11168})
       if (((v / 10) % 100) * (v % 10) >= g.KT) return v;
   }

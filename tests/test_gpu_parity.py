@@ -357,14 +357,15 @@ def test_every_gemv_variant(variant, G, monkeypatch):
 
 @pytest.mark.parametrize("K,N", [(4224, 136), (6144, 200), (8192, 72), (9728, 160), (11008, 88), (14336, 96)])
 def test_gemv_unsplit_deep_k(K, N):
-    """One and two rows over K of 33-112 k-tiles: the default plan covers the
-    whole K in one workgroup of 8 or 16 waves of up to 8 k-tiles each."""
+    """1-3 rows over K of 33-112 k-tiles (up to 6 rows at 76 k-tiles): the
+    default plan covers the whole K in one workgroup of 8 or 16 waves of up to
+    8 k-tiles each."""
     ops = _ops()
     G = 128
     t, d = _linear(K, N, G, seed=K % 1009 + N)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
-    for M in (1, 2):
+    for M in (1, 2, 3) if K != 9728 else (1, 3, 5, 6):
         assert ops.gemm_kernel(M, N, K, G) == "gemv_kernel"
         assert ops.workspace_bytes(M, N, K, G) == 0  # no split K
         x = oracle.make_activation(M, K, seed=M + 5)

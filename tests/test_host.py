@@ -98,14 +98,18 @@ def test_decode_routing(K, N, routes):
     assert got == routes, (K, N)
 
 
-def test_gemv_keeps_deep_k_unsplit_at_one_or_two_rows():
-    """Up to 128 k-tiles one GEMV workgroup covers K at 1-2 rows (no split-K
-    workspace); from 4 rows the 8-wave plan splits K again."""
+def test_gemv_keeps_deep_k_unsplit_at_few_rows():
+    """Up to 128 k-tiles one GEMV workgroup covers K at 1-3 rows (no split-K
+    workspace), and 65-80 k-tiles up to 6 rows; beyond that the 8-wave plans
+    split K again."""
     for K in (4224, 6144, 8192, 9728, 11008, 14336):
-        for M in (1, 2):
+        for M in (1, 2, 3):
             assert ops.gemm_kernel(M, 4096, K, 128) == "gemv_kernel"
             assert ops.workspace_bytes(M, 4096, K, 128) == 0, (M, K)
-    assert ops.workspace_bytes(4, 2560, 9728, 128) > 0
+    for M in (4, 5, 6):
+        assert ops.workspace_bytes(M, 2560, 9728, 128) == 0, M
+    assert ops.workspace_bytes(8, 2560, 9728, 128) > 0
+    assert ops.workspace_bytes(4, 4096, 14336, 128) > 0
     assert ops.workspace_bytes(1, 8192, 28672, 128) > 0  # 224 k-tiles still split
 
 
