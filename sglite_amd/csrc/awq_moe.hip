@@ -142,48 +142,76 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const float* __restri
 //   *num_post_pad                        off[E]
 // Rows whose id is outside [0, E) are dropped (fused.py:28-30 marks padded
 // tokens with -1).
+//
+// Wave w owns the contiguous rows [w * chunk, (w + 1) * chunk), so a row's
+// place in its bucket is the bucket offset, plus that expert's rows in lower
+// waves (a per-wave count and a prefix over waves), plus its rank inside its
+// own wave.  The rank needs no workgroup barrier: a wave takes its rows 64 at
+// a time in row order, the lanes of one expert find each other through a
+// per-wave lane mask in LDS, and the wave's LDS operations run in issue
+// order.  Sentinels are written in parallel over (expert, padding slot), block
+// experts over blocks (a binary search of the offsets).
 // ---------------------------------------------------------------------------
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kMaxExperts = 512;
-constexpr int kIdsPerThread = 4;  // ids held in registers per pass over the input
-constexpr int kAlignChunk = kAlignThreads * kIdsPerThread;
+constexpr int kAlignBatch = 4;  // 64-row groups a wave holds in registers per pass over its rows
 
 __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __restrict__ ids, int n, int E, int bs,
                                                               int32_t* __restrict__ sorted, int32_t* __restrict__ expert_ids,
                                                               int blocks_cap, int32_t* __restrict__ num_post_pad,
                                                               int32_t* __restrict__ offsets) {
+  // Per wave and expert: the wave's row count, then its first free position.
+  __shared__ int wpos[kAlignWaves][kMaxExperts];
+  // Per wave and expert: the lanes of the current 64-row group with that expert.
+  __shared__ uint64_t wmask[kAlignWaves][kMaxExperts];
   __shared__ int cnt[kMaxExperts];
   __shared__ int off[kMaxExperts + 1];
-  __shared__ int cursor[kMaxExperts];
   __shared__ int wtot[kAlignWaves];
-  // Lanes of wave w whose row goes to expert e, for the 1024 rows in flight.
-  __shared__ uint64_t wmask[kAlignWaves][kMaxExperts];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int chunk = ((n + kAlignWaves - 1) / kAlignWaves + 63) & ~63;
+  const int r0 = min(n, wave * chunk), r1 = min(n, r0 + chunk);
 
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
-  for (int i = tid; i < kAlignWaves * kMaxExperts; i += kAlignThreads) (&wmask[0][0])[i] = 0;
-  // Rows c0 + r * 1024 + tid, r < kIdsPerThread, loaded together (one
-  // round trip per chunk instead of one per row).
-  int er[kIdsPerThread];
-  auto load_chunk = [&](int c0) {
+  for (int q = tid; q < kAlignWaves * E; q += kAlignThreads) {
+    wpos[q / E][q % E] = 0;
+    wmask[q / E][q % E] = 0;
+  }
+  // The ids of kAlignBatch 64-row groups, loaded together (one round trip).
+  int er[kAlignBatch];
+  auto load_batch = [&](int b0) {
 #pragma unroll
-    for (int r = 0; r < kIdsPerThread; ++r) {
-      const int i = c0 + r * kAlignThreads + tid;
-      er[r] = i < n ? ids[i] : -1;
+    for (int r = 0; r < kAlignBatch; ++r) {
+      const int i = b0 + r * 64 + lane;
+      er[r] = i < r1 ? ids[i] : -1;
     }
   };
+  const bool one_batch = chunk <= 64 * kAlignBatch;  // the ids stay in registers between the passes
+  if (one_batch) load_batch(r0);
   __syncthreads();
-  for (int c0 = 0; c0 < n; c0 += kAlignChunk) {
-    load_chunk(c0);
+
+  // Pass 1: rows per (wave, expert).
+  for (int b0 = r0; b0 < r1; b0 += 64 * kAlignBatch) {  // wave-uniform
+    if (!one_batch) load_batch(b0);
 #pragma unroll
-    for (int r = 0; r < kIdsPerThread; ++r)
-      if (er[r] >= 0 && er[r] < E) atomicAdd(&cnt[er[r]], 1);
+    for (int r = 0; r < kAlignBatch; ++r)
+      if (er[r] >= 0 && er[r] < E) atomicAdd(&wpos[wave][er[r]], 1);
   }
   __syncthreads();
 
-  // Exclusive scan of the padded counts (E <= 1024: one element per thread).
-  const int pc = tid < E ? (cnt[tid] + bs - 1) / bs * bs : 0;
+  // Expert totals and each wave's offset inside its expert's rows.
+  int pc = 0;
+  if (tid < E) {
+    int sum = 0;
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) {
+      const int c = wpos[w][tid];
+      wpos[w][tid] = sum;
+      sum += c;
+    }
+    cnt[tid] = sum;
+    pc = (sum + bs - 1) / bs * bs;
+  }
+  // Exclusive scan of the padded counts (E <= 1024: one expert per thread).
   int incl = pc;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -196,48 +224,47 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(const int32_t* __r
   for (int w = 0; w < wave; ++w) base += wtot[w];
   if (tid < E) {
     off[tid] = base + incl - pc;
-    cursor[tid] = base + incl - pc;
+#pragma unroll
+    for (int w = 0; w < kAlignWaves; ++w) wpos[w][tid] += base + incl - pc;
   }
   if (tid == E - 1) off[E] = base + incl;
   __syncthreads();
 
+  // Offsets, sentinels and block experts.
   const int total = off[E];
   for (int e = tid; e <= E; e += kAlignThreads) offsets[e] = off[e];
   if (tid == 0) *num_post_pad = total;
-  for (int e = tid; e < E; e += kAlignThreads) {
-    for (int p = off[e] + cnt[e]; p < off[e + 1]; ++p) sorted[p] = n;
-    for (int b = off[e] / bs; b < off[e + 1] / bs; ++b) expert_ids[b] = e;
+  auto bucket_of = [&](int p) {  // the expert e with off[e] <= p < off[e + 1], for p < total
+    int lo = 0, hi = E;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= p) lo = mid;
+      else hi = mid;
+    }
+    return lo;
+  };
+  for (int q = tid; q < E * bs; q += kAlignThreads) {  // padding slot q % bs of expert q / bs
+    const int e = q / bs, p = off[e] + cnt[e] + q % bs;
+    if (p < off[e + 1]) sorted[p] = n;
   }
-  for (int b = total / bs + tid; b < blocks_cap; b += kAlignThreads) expert_ids[b] = -1;
+  for (int b = tid; b < blocks_cap; b += kAlignThreads) expert_ids[b] = b * bs < total ? bucket_of(b * bs) : -1;
 
-  // Stable scatter, 1024 rows at a time: a row's position is its bucket's
-  // cursor, plus the rows of the same expert in lower waves, plus those in
-  // lower lanes of its own wave (all popcounts of the lane masks).
-  for (int c0 = 0; c0 < n; c0 += kAlignChunk) {
-    if (c0 > 0 || n > kAlignChunk) load_chunk(c0);  // a single chunk is still in registers
+  // Pass 2: stable scatter, wave by wave, 64 rows at a time.
+  for (int b0 = r0; b0 < r1; b0 += 64 * kAlignBatch) {  // wave-uniform
+    if (!one_batch) load_batch(b0);
 #pragma unroll
-    for (int r = 0; r < kIdsPerThread; ++r) {
-      if (c0 + r * kAlignThreads >= n) break;  // uniform
-      const int i = c0 + r * kAlignThreads + tid;
+    for (int r = 0; r < kAlignBatch; ++r) {
       const int e = er[r];
       const bool valid = e >= 0 && e < E;
       if (valid) atomicOr((unsigned long long*)&wmask[wave][e], 1ull << lane);
-      __syncthreads();
       if (valid) {
         const uint64_t m = wmask[wave][e];
-        int pos = cursor[e] + __popcll(m & lanes_below(lane));
-        for (int w = 0; w < wave; ++w) pos += __popcll(wmask[w][e]);
-        sorted[pos] = i;
+        sorted[wpos[wave][e] + __popcll(m & lanes_below(lane))] = b0 + r * 64 + lane;
+        if ((m & lanes_below(lane)) == 0) {  // lowest lane of the expert's group
+          wpos[wave][e] += __popcll(m);
+          wmask[wave][e] = 0;
+        }
       }
-      __syncthreads();
-      for (int ee = tid; ee < E; ee += kAlignThreads) {
-        int s = 0;
-        for (int w = 0; w < kAlignWaves; ++w) s += __popcll(wmask[w][ee]);
-        cursor[ee] += s;
-      }
-      __syncthreads();
-      if (valid) wmask[wave][e] = 0;  // every lane of the group writes the same zero
-      __syncthreads();
     }
   }
 }
