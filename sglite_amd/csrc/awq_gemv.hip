@@ -15,7 +15,11 @@
 // (rows >= M read row M - 1; their outputs are never stored).
 //
 // Per k-block the weights are dequantised exactly (Dq<DT>::word, the same
-// rounding as the oracle) into the MFMA A operand and accumulated in fp32;
+// rounding as the oracle) into the MFMA A operand and accumulated in fp32 --
+// or, for single-row GEMMs, the A operand is the biased weight B + q (one
+// v_and_or_b32 per weight pair) and the group's scale and zero-point term
+// -s (B + z) * sum(x) are applied in fp32 (the workgroup sums each row's
+// k-tile once while it stages the slice), a third of the vector work;
 // the WK waves' partial sums are reduced through LDS by all threads, and
 // split-K slices are combined across workgroups with the same fence-free
 // atomic handoff as the wider decode kernel (device-scope exchanges and an
@@ -26,6 +30,7 @@
 // and gptq_marlin_gemm (marlin_utils.py:388-410) for batches of up to 32 rows
 // whose quantisation groups span whole 128-row tiles (G = 128 or G = K).
 #include <algorithm>
+#include <type_traits>
 
 #include "awq_device.h"
 #include "awq_epilogue.h"
@@ -34,6 +39,41 @@
 namespace sgl_awq {
 
 namespace {
+
+// fp32 value of a 16-bit activation or scale element.
+template <typename DT>
+__device__ __forceinline__ float elem_f32(uint32_t bits);
+template <>
+__device__ __forceinline__ float elem_f32<F16>(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+template <>
+__device__ __forceinline__ float elem_f32<BF16>(uint32_t bits) {
+  return __builtin_bit_cast(float, bits << 16);
+}
+
+// Sum over each aligned 16-lane row of the wave, left in the row's lane 15
+// (DPP row shifts: no LDS round trip).
+__device__ __forceinline__ float row16_sum(float v) {
+  auto shr = [](float x, auto ctrl, auto bank_mask) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl)::value,
+                                                                 0xf, decltype(bank_mask)::value, false));
+  };
+  v += shr(v, std::integral_constant<int, 0x111>{}, std::integral_constant<int, 0xf>{});  // row_shr:1
+  v += shr(v, std::integral_constant<int, 0x112>{}, std::integral_constant<int, 0xf>{});  // row_shr:2
+  v += shr(v, std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xe>{});  // row_shr:4
+  v += shr(v, std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xc>{});  // row_shr:8
+  return v;
+}
+
+// Sum of the eight 16-bit elements of a 16-byte chunk, in fp32.
+template <typename DT>
+__device__ __forceinline__ float chunk_sum(const u32x4& v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s += elem_f32<DT>(v[i] & 0xFFFFu) + elem_f32<DT>(v[i] >> 16);
+  return s;
+}
 
 // Epilogue of a gemv workgroup with a fused gate/up activation: wave wn
 // holds gate tile t = blockIdx.x * WN + wn in slot 0 and its up tile
@@ -133,7 +173,7 @@ __device__ __forceinline__ void gemv_paired_epilogue(const f32x4 (&acc)[MT][2], 
   if (threadIdx.x == 0) __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NTW, int WN, int WK, int KPW, int MT, int XPT, typename DT>
+template <int NTW, int WN, int WK, int KPW, int MT, int XPT, typename DT, bool BIASED>
 __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     const typename DT::elem* __restrict__ x, const u32x4* __restrict__ wt, const uint16_t* __restrict__ s_r,
     const uint64_t* __restrict__ z_r, const typename DT::elem* __restrict__ bias, typename DT::elem* __restrict__ out,
@@ -174,7 +214,8 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   // (one quantisation group per 128-row tile: G >= 128)
   u32x4 q[KPW][NTW];
   uint32_t zw[KPW][NTW];
-  uint16_t sb[KPW][NTW];
+  uint16_t sb[KPW][NTW];   // scale of the lane's own column c
+  uint2 s4[KPW][NTW];      // (biased operand) scales of the lane's output columns 4 lg .. 4 lg + 3
   // With a fused gate/up activation (two tiles per wave) the wave's tiles
   // are gate tile t = blockIdx.x * WN + wn and its up tile t + NT / 2.
   const bool paired = NTW == 2 && act != kActNone;
@@ -199,23 +240,43 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
       const uint32_t gi = goff[j] + g;
       zw[i][j] = ld_off<uint32_t>(z_r, gi * 8u + (uint32_t)(c >> 3) * 4u);
       sb[i][j] = ld_off<uint16_t>(s_r, (gi * 16u + c) * 2u);
+      if constexpr (BIASED) s4[i][j] = ld_off<uint2>(s_r, (gi * 16u + 4u * (uint32_t)lg) * 2u);
     }
   }
 
   // ---- publish the activation slice ----------------------------------------
+  // With the biased operand, also the sum of every (row, k-tile) of the
+  // slice, xsum[kt * M + m]: the 16 chunks of one row's k-tile are 16
+  // consecutive threads (an aligned quarter wave, as cpr and NTHREADS are
+  // multiples of 16).
   _Float16* xs = (_Float16*)smem;
+  float* xsum = (float*)((char*)smem + ((M * rs * 2 + 15) & ~15));
 #pragma unroll
   for (int r = 0; r < XPT; ++r) {
     const int qi = threadIdx.x + r * NTHREADS;
-    if (qi < M * cpr) {
-      const int m = qi / cpr, kk = (qi % cpr) * 8;
-      const bool kval = kt_begin * 128 + kk < K;
-      *(u32x4*)(xs + m * rs + kk) = kval ? xr[r] : u32x4{0u, 0u, 0u, 0u};
+    const bool live = qi < M * cpr;
+    const int m = live ? qi / cpr : 0, kk = live ? (qi % cpr) * 8 : 0;
+    const u32x4 v = live && kt_begin * 128 + kk < K ? xr[r] : u32x4{0u, 0u, 0u, 0u};
+    if (live) *(u32x4*)(xs + m * rs + kk) = v;
+    if constexpr (BIASED) {
+      const float sum = row16_sum(chunk_sum<DT>(v));
+      if (live && (qi & 15) == 15) xsum[(kk >> 7) * M + m] = sum;
     }
   }
   __syncthreads();
 
   // ---- compute ---------------------------------------------------------------
+  // Exact path: per k-block the weights are dequantised to (q - z) * s with
+  // the oracle's rounding (Dq<DT>::word, 13 VALU operations per 8 weights)
+  // into the MFMA A operand, accumulated in fp32.
+  // Biased path (single-row GEMMs, where the vector work of dequantising is
+  // the larger part of the kernel's time): the MFMAs take the biased weights
+  // B + q straight from the nibbles (one v_and_or_b32 per pair), so
+  //   sum_k (q - z) s x = s * sum_k (B + q) x - s (B + z) * sum_k x :
+  // the first term is scaled into the fp32 accumulator per k-tile (the lane's
+  // four output columns' scales), the second is one fp32 MFMA per four
+  // k-tiles, with -s (B + z) of the lane's own column in k-tile slot lg as
+  // the A operand and the row sums of slot lg as the B operand.
   f32x4 acc[MT][NTW];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -224,23 +285,88 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   int xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + c, M - 1) * rs + lg * 8;
+  if constexpr (!BIASED) {
 #pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    if (i < kpw) {
-      const int kl = (wk + WK * i) * 128;  // k offset inside the slice
-      ZS zs[NTW];
+    for (int i = 0; i < KPW; ++i) {
+      if (i < kpw) {
+        const int kl = (wk + WK * i) * 128;  // k offset inside the slice
+        ZS zs[NTW];
 #pragma unroll
-      for (int j = 0; j < NTW; ++j) zs[j] = Dq<DT>::make((zw[i][j] >> (4 * (c & 7))) & 0xFu, sb[i][j]);
+        for (int j = 0; j < NTW; ++j) zs[j] = Dq<DT>::make((zw[i][j] >> (4 * (c & 7))) & 0xFu, sb[i][j]);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        V8 av[NTW];
+        for (int w = 0; w < 4; ++w) {
+          V8 av[NTW];
 #pragma unroll
-        for (int j = 0; j < NTW; ++j) av[j] = Dq<DT>::word(q[i][j][w], zs[j], dk);
+          for (int j = 0; j < NTW; ++j) av[j] = Dq<DT>::word(q[i][j][w], zs[j], dk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow[mt] + kl + 32 * w));
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
+          }
+        }
+      }
+    }
+  } else {
+    const uint32_t kMagic = opaque_vgpr(Raw<DT>::kMagic);
+    const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Every k-tile's MFMAs first (each starts as soon as its loads land), the
+    // scaling after all of them, so that no VALU operation waits on the MFMA
+    // result just issued.
+    f32x4 t[KPW][MT][NTW];
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      if (i < kpw) {
+        const int kl = (wk + WK * i) * 128;  // k offset inside the slice
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          V8 av[NTW];
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) av[j] = biased_word<DT>(q[i][j][w], dk.lo, kMagic);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow[mt] + kl + 32 * w));
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) t[i][mt][j] = mfma16x16x32(av[j], bx, w == 0 ? zero4 : t[i][mt][j]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      if (i < kpw) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const float sc[4] = {elem_f32<DT>(s4[i][j].x & 0xFFFFu), elem_f32<DT>(s4[i][j].x >> 16),
+                               elem_f32<DT>(s4[i][j].y & 0xFFFFu), elem_f32<DT>(s4[i][j].y >> 16)};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mt][j][r] = fmaf(sc[r], t[i][mt][j][r], acc[mt][j][r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int ch = 0; ch < (KPW + 3) / 4; ++ch) {
+      if (4 * ch < kpw) {
+        float u[NTW];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) u[j] = 0.f;
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = 4 * ch + ii;
+          if (i < KPW && lg == ii && i < kpw) {
+#pragma unroll
+            for (int j = 0; j < NTW; ++j)
+              u[j] = -(elem_f32<DT>(sb[i][j]) * (Raw<DT>::kBias + (float)((zw[i][j] >> (4 * (c & 7))) & 0xFu)));
+          }
+        }
+        const int kts = wk + WK * min(4 * ch + lg, kpw - 1);  // k-tile of slot lg in the slice
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow[mt] + kl + 32 * w));
+          const float sv = xsum[kts * M + min(mt * 16 + c, M - 1)];
 #pragma unroll
-          for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
+          for (int j = 0; j < NTW; ++j) acc[mt][j] = mfma16x16x4f32(u[j], sv, acc[mt][j]);
         }
       }
     }
@@ -361,9 +487,34 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   const int xpt = p.xpt;
   dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
   const size_t lds = (size_t)p.lds_bytes;
+  // Single-row plain GEMMs on one-tile waves take the biased operand (same-box
+  // sweep on MI355X: 4-12% faster at M = 1, slower from M = 2 on and with a
+  // fused activation).  At one row the slice needs at most 2 loads per thread.
+  const bool biased = g.M == 1 && act == kActNone && ntw == 1 && xpt <= 2;
+#define SGL_GEMV_B(WN_, WK_, KPW_, XPT_)                                                                            \
+  if (biased && wn == WN_ && wk == WK_ && kpw == KPW_ && xpt == XPT_) {                                             \
+    hipLaunchKernelGGL((gemv_kernel<1, WN_, WK_, KPW_, 1, XPT_, DT, true>), grid, dim3(64 * WN_ * WK_), lds, s,      \
+                       (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters,  \
+                       (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks, act); \
+    return hipGetLastError();                                                                                     \
+  }
+#define SGL_GEMV_B2(WN_, WK_, KPW_) SGL_GEMV_B(WN_, WK_, KPW_, 1) SGL_GEMV_B(WN_, WK_, KPW_, 2)
+  SGL_GEMV_B2(1, 4, 8)
+  SGL_GEMV_B2(1, 8, 4)
+  SGL_GEMV_B2(1, 8, 3)
+  SGL_GEMV_B2(2, 8, 3)
+  SGL_GEMV_B2(2, 8, 4)
+  SGL_GEMV_B2(1, 8, 6)
+  SGL_GEMV_B2(1, 8, 8)
+  SGL_GEMV_B2(1, 16, 5)
+  SGL_GEMV_B2(1, 16, 6)
+  SGL_GEMV_B2(1, 16, 8)
+  SGL_GEMV_B2(4, 4, 4)
+#undef SGL_GEMV_B2
+#undef SGL_GEMV_B
 #define SGL_GEMV(NTW_, WN_, WK_, KPW_, MT_, XPT_)                                                                  \
-  if (ntw == NTW_ && wn == WN_ && wk == WK_ && kpw == KPW_ && mt == MT_ && xpt == XPT_) {                          \
-    hipLaunchKernelGGL((gemv_kernel<NTW_, WN_, WK_, KPW_, MT_, XPT_, DT>), grid, dim3(64 * WN_ * WK_), lds, s,       \
+  if (!biased && ntw == NTW_ && wn == WN_ && wk == WK_ && kpw == KPW_ && mt == MT_ && xpt == XPT_) {               \
+    hipLaunchKernelGGL((gemv_kernel<NTW_, WN_, WK_, KPW_, MT_, XPT_, DT, false>), grid, dim3(64 * WN_ * WK_), lds, s,\
                        (const E*)x, (const u32x4*)w, sbase, zbase, (const E*)bias, (E*)out, (float*)ws, counters,  \
                        (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks, act); \
     return hipGetLastError();                                                                                     \
