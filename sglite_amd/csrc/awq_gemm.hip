@@ -62,10 +62,11 @@ GemvSplit gemv_split(const Geom& g, int v, int64_t ks) {
   for (ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT)); ks <= g.KT; ++ks) {
     const int64_t ktc = (g.KT + ks - 1) / ks;
     const int64_t xpt = (g.M * ktc * 16 + threads - 1) / threads;
-    // activation slice (rows padded by 8 halves), at one row its per-k-tile
-    // sums (the biased-operand path), then (reusing the space) the k-waves'
-    // partial sums
-    const int64_t lds = std::max<int64_t>(((g.M * (ktc * 128 + 8) * 2 + 15) & ~int64_t(15)) + (g.M == 1 ? ktc * 4 : 0),
+    // activation slice (rows padded by 8 halves), up to 3 rows its per-k-tile
+    // row sums (the biased-operand path), then (reusing the space) the
+    // k-waves' partial sums
+    const int64_t lds = std::max<int64_t>(((g.M * (ktc * 128 + 8) * 2 + 15) & ~int64_t(15)) +
+                                              (g.M <= 3 ? ktc * g.M * 4 : 0),
                                           (int64_t)wk * wn * mt * ntw * 1024);
     if ((ktc + wk - 1) / wk <= kpw && xpt <= 8 && lds <= kGemvLdsMax) return {(g.KT + ktc - 1) / ktc, ktc, xpt, lds};
   }

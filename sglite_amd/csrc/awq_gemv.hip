@@ -16,7 +16,7 @@
 //
 // Per k-block the weights are dequantised exactly (Dq<DT>::word, the same
 // rounding as the oracle) into the MFMA A operand and accumulated in fp32 --
-// or, for single-row GEMMs, the A operand is the biased weight B + q (one
+// or, for GEMMs of up to 3 rows, the A operand is the biased weight B + q (one
 // v_and_or_b32 per weight pair) and the group's scale and zero-point term
 // -s (B + z) * sum(x) are applied in fp32 (the workgroup sums each row's
 // k-tile once while it stages the slice), a third of the vector work;
@@ -66,12 +66,28 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Sum of the eight 16-bit elements of a 16-byte chunk, in fp32.
+// Sum of the eight 16-bit elements of a 16-byte chunk, in fp32 (fp16: four
+// v_dot2_f32_f16 against (1, 1)).  The words are named one by one: hipcc
+// (ROCm 7.2) miscompiles __builtin_bit_cast of v[i] inside an unrolled loop
+// into four uses of the first word.
 template <typename DT>
-__device__ __forceinline__ float chunk_sum(const u32x4& v) {
+__device__ __forceinline__ float chunk_sum(u32x4 v);
+template <>
+__device__ __forceinline__ float chunk_sum<F16>(u32x4 v) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
+  float s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w0), one, 0.f, false);
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w1), one, s, false);
+  s = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w2), one, s, false);
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w3), one, s, false);
+}
+template <>
+__device__ __forceinline__ float chunk_sum<BF16>(u32x4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s += elem_f32<DT>(v[i] & 0xFFFFu) + elem_f32<DT>(v[i] >> 16);
+  for (int i = 0; i < 4; ++i) s += elem_f32<BF16>(w[i] & 0xFFFFu) + elem_f32<BF16>(w[i] >> 16);
   return s;
 }
 
@@ -269,8 +285,8 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   // Exact path: per k-block the weights are dequantised to (q - z) * s with
   // the oracle's rounding (Dq<DT>::word, 13 VALU operations per 8 weights)
   // into the MFMA A operand, accumulated in fp32.
-  // Biased path (single-row GEMMs, where the vector work of dequantising is
-  // the larger part of the kernel's time): the MFMAs take the biased weights
+  // Biased path (GEMMs of up to 3 rows, where the vector work of dequantising
+  // weighs most against the rest of the kernel): the MFMAs take the biased weights
   // B + q straight from the nibbles (one v_and_or_b32 per pair), so
   //   sum_k (q - z) s x = s * sum_k (B + q) x - s (B + z) * sum_k x :
   // the first term is scaled into the fp32 accumulator per k-tile (the lane's
@@ -487,10 +503,10 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   const int xpt = p.xpt;
   dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
   const size_t lds = (size_t)p.lds_bytes;
-  // Single-row plain GEMMs on one-tile waves take the biased operand (same-box
-  // sweep on MI355X: 4-12% faster at M = 1, slower from M = 2 on and with a
-  // fused activation).  At one row the slice needs at most 2 loads per thread.
-  const bool biased = g.M == 1 && act == kActNone && ntw == 1 && xpt <= 2;
+  // Plain GEMMs of up to 3 rows on one-tile waves take the biased operand
+  // (same-box sweep on MI355X: 4-12% faster at M = 1, up to 7% at M = 2-3;
+  // from 4 rows on, and with a fused activation, mixed or slower).
+  const bool biased = g.M <= 3 && act == kActNone && ntw == 1;
 #define SGL_GEMV_B(WN_, WK_, KPW_, XPT_)                                                                            \
   if (biased && wn == WN_ && wk == WK_ && kpw == KPW_ && xpt == XPT_) {                                             \
     hipLaunchKernelGGL((gemv_kernel<1, WN_, WK_, KPW_, 1, XPT_, DT, true>), grid, dim3(64 * WN_ * WK_), lds, s,      \
@@ -498,7 +514,8 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
                        (int)g.M, (int)g.N, (int)g.K, (int)g.NT, (int)g.KT, (int)g.NG, g.gshift, p.ktc, p.ks, act); \
     return hipGetLastError();                                                                                     \
   }
-#define SGL_GEMV_B2(WN_, WK_, KPW_) SGL_GEMV_B(WN_, WK_, KPW_, 1) SGL_GEMV_B(WN_, WK_, KPW_, 2)
+#define SGL_GEMV_B2(WN_, WK_, KPW_) \
+  SGL_GEMV_B(WN_, WK_, KPW_, 1) SGL_GEMV_B(WN_, WK_, KPW_, 2) SGL_GEMV_B(WN_, WK_, KPW_, 4) SGL_GEMV_B(WN_, WK_, KPW_, 8)
   SGL_GEMV_B2(1, 4, 8)
   SGL_GEMV_B2(1, 8, 4)
   SGL_GEMV_B2(1, 8, 3)

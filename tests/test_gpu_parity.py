@@ -335,8 +335,9 @@ def test_decode_bf16_variants(M, monkeypatch):
 @pytest.mark.parametrize("G", [128, -1])
 def test_every_gemv_variant(variant, G, monkeypatch):
     """Each small-batch GEMV instantiation, with and without cross-workgroup
-    split-K, for batch sizes over both m-tile counts (1..32 rows), on a K with a
-    partial last 128-row tile and N % 16 == 8."""
+    split-K, for batch sizes over both m-tile counts (1..32 rows; 1 and 3 rows
+    take the biased-operand arithmetic), on a K with a partial last 128-row
+    tile and N % 16 == 8."""
     ops = _ops()
     K, N = 2432, 200
     t, d = _linear(K, N, G, seed=variant % 997 + (G if G > 0 else 7))
@@ -346,7 +347,7 @@ def test_every_gemv_variant(variant, G, monkeypatch):
     monkeypatch.setenv("SGL_AWQ_GEMV_VARIANT", str(variant))
     for ks in (1, 3):
         monkeypatch.setenv("SGL_AWQ_GEMV_KS", str(ks))
-        for M in (1, 4, 16, 17, 32):
+        for M in (1, 3, 4, 16, 17, 32):
             x = oracle.make_activation(M, K, seed=M + ks)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
             ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
@@ -375,7 +376,7 @@ def test_gemv_unsplit_deep_k(K, N):
         assert ok, (K, N, M, err, mx)
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 def test_gemv_bf16_and_bias(M):
     ops = _ops()
     K, N, G = 4096, 136, 128
