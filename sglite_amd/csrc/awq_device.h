@@ -135,6 +135,19 @@ struct Dq<F16> {
                      __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3)};
     return __builtin_bit_cast(f16x8, r);
   }
+  // The exact integers q - z (no scaling): 9 VALU operations per word, for
+  // kernels that apply the group scale to the fp32 sums instead.
+  __device__ __forceinline__ static f16x8 word_q_minus_z(uint32_t w, const ZS& zs, const DqK& k) {
+    const f16x2 inv16 = __builtin_bit_cast(f16x2, 0x2C002C00u);  // (1/16, 1/16)
+    const uint32_t w8 = w >> 8;
+    const f16x2 h0 = __builtin_bit_cast(f16x2, and_or(w, k.lo, k.magic)) - zs.zb;
+    const f16x2 h1 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, and_or(w, k.hi, k.magic)), inv16, zs.zh);
+    const f16x2 h2 = __builtin_bit_cast(f16x2, and_or(w8, k.lo, k.magic)) - zs.zb;
+    const f16x2 h3 = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, and_or(w8, k.hi, k.magic)), inv16, zs.zh);
+    const u32x4 r = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                     __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3)};
+    return __builtin_bit_cast(f16x8, r);
+  }
 };
 
 // bf16: (q - z) * s is exact in fp32 (4-bit by 8-bit significands) and the

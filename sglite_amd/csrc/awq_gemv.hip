@@ -231,7 +231,7 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   u32x4 q[KPW][NTW];
   uint32_t zw[KPW][NTW];
   uint16_t sb[KPW][NTW];   // scale of the lane's own column c
-  uint2 s4[KPW][NTW];      // (biased operand) scales of the lane's output columns 4 lg .. 4 lg + 3
+  uint2 s4[KPW][NTW];      // scales of the lane's output columns 4 lg .. 4 lg + 3 (fp32 scaling)
   // With a fused gate/up activation (two tiles per wave) the wave's tiles
   // are gate tile t = blockIdx.x * WN + wn and its up tile t + NT / 2.
   const bool paired = NTW == 2 && act != kActNone;
@@ -256,7 +256,8 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
       const uint32_t gi = goff[j] + g;
       zw[i][j] = ld_off<uint32_t>(z_r, gi * 8u + (uint32_t)(c >> 3) * 4u);
       sb[i][j] = ld_off<uint16_t>(s_r, (gi * 16u + c) * 2u);
-      if constexpr (BIASED) s4[i][j] = ld_off<uint2>(s_r, (gi * 16u + 4u * (uint32_t)lg) * 2u);
+      if constexpr (BIASED || std::is_same_v<DT, F16>)
+        s4[i][j] = ld_off<uint2>(s_r, (gi * 16u + 4u * (uint32_t)lg) * 2u);
     }
   }
 
@@ -301,7 +302,48 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   int xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + c, M - 1) * rs + lg * 8;
-  if constexpr (!BIASED) {
+  if constexpr (!BIASED && std::is_same_v<DT, F16>) {
+    // fp16: the exact integers q - z (two VALU operations per weight pair)
+    // into the MFMAs, each k-tile's sum scaled in fp32 by the lane's four
+    // output-column scales, after all the k-tiles' MFMAs are issued.
+    const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 t[KPW][MT][NTW];
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      if (i < kpw) {
+        const int kl = (wk + WK * i) * 128;  // k offset inside the slice
+        ZS zs[NTW];
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) zs[j] = Dq<DT>::make((zw[i][j] >> (4 * (c & 7))) & 0xFu, sb[i][j]);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          V8 av[NTW];
+#pragma unroll
+          for (int j = 0; j < NTW; ++j) av[j] = Dq<DT>::word_q_minus_z(q[i][j][w], zs[j], dk);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const V8 bx = __builtin_bit_cast(V8, *(const u32x4*)(xs + xrow[mt] + kl + 32 * w));
+#pragma unroll
+            for (int j = 0; j < NTW; ++j) t[i][mt][j] = mfma16x16x32(av[j], bx, w == 0 ? zero4 : t[i][mt][j]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      if (i < kpw) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          const float sc[4] = {elem_f32<DT>(s4[i][j].x & 0xFFFFu), elem_f32<DT>(s4[i][j].x >> 16),
+                               elem_f32<DT>(s4[i][j].y & 0xFFFFu), elem_f32<DT>(s4[i][j].y >> 16)};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[mt][j][r] = fmaf(sc[r], t[i][mt][j][r], acc[mt][j][r]);
+        }
+      }
+    }
+  } else if constexpr (!BIASED) {
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       if (i < kpw) {
