@@ -14,12 +14,14 @@
 // weights' HBM latency.  MFMA B fragments are then ds_read_b128 of that slice
 // (rows >= M read row M - 1; their outputs are never stored).
 //
-// Per k-block the weights are dequantised exactly (Dq<DT>::word, the same
-// rounding as the oracle) into the MFMA A operand and accumulated in fp32 --
-// or, for GEMMs of up to 3 rows, the A operand is the biased weight B + q (one
-// v_and_or_b32 per weight pair) and the group's scale and zero-point term
-// -s (B + z) * sum(x) are applied in fp32 (the workgroup sums each row's
-// k-tile once while it stages the slice), a third of the vector work;
+// The MFMA A operand is, per k-tile (one quantisation group):
+//   * plain GEMMs of up to 3 rows: the biased weight B + q (one v_and_or_b32
+//     per weight pair), with the group's scale and the zero-point term
+//     -s (B + z) * sum(x) applied in fp32 (the workgroup sums each row's
+//     k-tile once while it stages the slice);
+//   * other fp16 GEMMs: the exact integers q - z, the sum scaled in fp32;
+//   * bf16: the weight dequantised to (q - z) * s with the oracle's rounding
+//     (Dq<DT>::word);
 // the WK waves' partial sums are reduced through LDS by all threads, and
 // split-K slices are combined across workgroups with the same fence-free
 // atomic handoff as the wider decode kernel (device-scope exchanges and an
@@ -283,9 +285,10 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   __syncthreads();
 
   // ---- compute ---------------------------------------------------------------
-  // Exact path: per k-block the weights are dequantised to (q - z) * s with
-  // the oracle's rounding (Dq<DT>::word, 13 VALU operations per 8 weights)
-  // into the MFMA A operand, accumulated in fp32.
+  // bf16 (not biased): per k-block the weights are dequantised to (q - z) * s
+  // with the oracle's rounding (Dq<DT>::word, 13 VALU operations per 8
+  // weights) into the MFMA A operand, accumulated in fp32; fp16 takes the
+  // integers q - z (9 operations) and scales each k-tile's sum in fp32.
   // Biased path (GEMMs of up to 3 rows, where the vector work of dequantising
   // weighs most against the rest of the kernel): the MFMAs take the biased weights
   // B + q straight from the nibbles (one v_and_or_b32 per pair), so
