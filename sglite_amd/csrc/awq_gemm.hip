@@ -95,6 +95,12 @@ int64_t gemv_min_ks(const Geom& g, int v) {
 // variants over the Qwen3-4B, Llama-3-8B and Llama-3-70B shapes.)
 int gemv_default_variant(const Geom& g, int act) {
   if (act) return g.M <= 4 ? 21044 : 21084;
+  // 1025-1280 column tiles (the Qwen3-4B gate_up, 1216) and K within 21
+  // k-tiles, 2+ rows: five column tiles per workgroup (5 x 3 waves of 7
+  // k-tiles) put one workgroup on each CU, which then stages the activation
+  // slice once instead of five times (12.2 -> 10.1 us at M = 8; at M = 1 and
+  // on layers whose workgroup count misses 256 it is slower).
+  if (g.M >= 2 && g.NT > 1024 && g.NT <= 1280 && g.KT <= 21) return 15037;
   if (g.KT > 24 && g.KT <= 128 && (g.M <= 3 || (g.M <= 6 && g.KT > 64 && g.KT <= 80))) {
     for (int v : {11084, 11086, 11088, 11165, 11166, 11168})
       if (((v / 10) % 100) * (v % 10) >= g.KT) return v;
