@@ -201,8 +201,9 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   using ZS = typename Dq<DT>::ZS;
   constexpr int NTHREADS = 64 * WN * WK;
   constexpr int NTG = WN * NTW;  // column tiles of the workgroup
-  // LDS: the activation slice (M x ktc*128 halves, row stride ktc*128 + 8), then
-  // (after a barrier) the WK partial sums of every output quad.
+  // LDS: the activation slice (M x ktc*128 halves, row stride ktc*128 + 8),
+  // on the biased path its per-(row, k-tile) sums (16-byte aligned), then
+  // (after a barrier, over both) the WK partial sums of every output quad.
   extern __shared__ u32x4 smem[];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
