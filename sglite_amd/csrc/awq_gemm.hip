@@ -87,14 +87,19 @@ int64_t gemv_min_ks(const Geom& g, int v) {
 // (Qwen3-4B down 8.4 -> 7.5 us at M = 1, 9.9 -> 9.3 us at M = 6; Llama-3-8B
 // down 12.2 -> 11.0 us and 70B-sized o 12.5 -> 10.9 us at M = 1; at 4 rows
 // and more on other depths the larger activation slices lose).  One column
-// tile per workgroup up to 4 rows; from 5 rows (7 on layers of >= 1024 column tiles, where the
-// workgroup count matters more) two column tiles share a workgroup of 16
-// waves, which halves the activation slices staged per weight byte.  With a
-// fused gate/up activation a workgroup holds one gate tile and its up tile:
-// 4 waves at up to 4 rows, 8 waves at 5-8 rows.  (Graph-replay sweep of the
-// variants over the Qwen3-4B, Llama-3-8B and Llama-3-70B shapes.)
+// tile per workgroup up to 4 rows; from 5 rows (7 on layers of >= 1024 column
+// tiles, where the workgroup count matters more) two column tiles share a
+// workgroup of 16 waves, which halves the activation slices staged per weight
+// byte.  With a fused gate/up activation a workgroup holds one gate tile and
+// its up tile, in 8 waves of 3 or 4 k-tiles by the same rule (the Qwen3-4B
+// gate_up, 20 k-tiles, unsplit: 12.3 -> 9.9 us at M = 1, 13.8 -> 10.9 us at
+// M = 4).  (Graph-replay sweep of the variants over the Qwen3-4B, Llama-3-8B
+// and Llama-3-70B shapes.)
 int gemv_default_variant(const Geom& g, int act) {
-  if (act) return g.M <= 4 ? 21044 : 21084;
+  if (act) {
+    const int64_t k3 = gemv_split(g, 21083, gemv_min_ks(g, 21083)).ks, k4 = gemv_split(g, 21084, gemv_min_ks(g, 21084)).ks;
+    return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? 21083 : 21084;
+  }
   // 1025-1280 column tiles (the Qwen3-4B gate_up, 1216) and K within 21
   // k-tiles, 2+ rows: five column tiles per workgroup (5 x 3 waves of 7
   // k-tiles) put one workgroup on each CU, which then stages the activation
