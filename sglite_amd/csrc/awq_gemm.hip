@@ -97,6 +97,11 @@ int64_t gemv_min_ks(const Geom& g, int v) {
 // and Llama-3-70B shapes.)
 int gemv_default_variant(const Geom& g, int act) {
   if (act) {
+    // 7+ rows on 513-768 gate/up pairs with K within 20 k-tiles (the Qwen3-4B
+    // gate_up): three pairs per workgroup (3 x 5 waves of 4 k-tiles), 203
+    // workgroups that each stage the activation slice once (13.4 -> 11.4 us
+    // at M = 8; even at M = 6, slower at M = 4).
+    if (g.M >= 7 && g.NT > 1024 && g.NT <= 1536 && g.KT <= 20) return 23054;
     const int64_t k3 = gemv_split(g, 21083, gemv_min_ks(g, 21083)).ks, k4 = gemv_split(g, 21084, gemv_min_ks(g, 21084)).ks;
     return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? 21083 : 21084;
   }

@@ -606,6 +606,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
   SGL_GEMV_M(2, 4, 4, 2)
   SGL_GEMV_M(1, 4, 4, 4)
   SGL_GEMV_M(1, 5, 3, 7)
+  SGL_GEMV_M(2, 3, 5, 4)
 #undef SGL_GEMV_M
 #undef SGL_GEMV_X
 #undef SGL_GEMV
@@ -618,7 +619,7 @@ hipError_t launch_gemv_dt(const GemmPlan& p, const void* x, const void* w, const
 bool gemv_variant_ok(int v) {
   switch (v) {
     case 11048: case 11083: case 11084: case 11086: case 11088: case 11165: case 11166: case 11168: case 12083:
-    case 12084: case 15037: case 21044: case 21083: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
+    case 12084: case 15037: case 23054: case 21044: case 21083: case 21084: case 22028: case 22044: case 24024: case 24042: case 14044:
       return true;
     default:
       return false;

@@ -74,7 +74,7 @@ def test_fused_activation_with_bias(act, M, monkeypatch):
     _check(M, 1024, 272, act=act, with_bias=True, monkeypatch=monkeypatch)
 
 
-@pytest.mark.parametrize("variant", [21044, 21083, 21084, 22028, 22044, 24024, 24042])
+@pytest.mark.parametrize("variant", [21044, 21083, 21084, 22028, 22044, 23054, 24024, 24042])
 @pytest.mark.parametrize("M", [1, 8])
 def test_every_two_tile_gemv_shape(variant, M, monkeypatch):
     _check(M, 4096, 1040, env={"SGL_AWQ_GEMV_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 8}, kernel="gemv_kernel",

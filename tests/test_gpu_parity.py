@@ -331,7 +331,7 @@ def test_decode_bf16_variants(M, monkeypatch):
 
 
 @pytest.mark.parametrize("variant", [11048, 11083, 11084, 11086, 11088, 11165, 11166, 11168, 12083, 12084, 15037,
-                                     21044, 21083, 21084, 22028, 22044, 24024, 24042, 14044])
+                                     21044, 21083, 21084, 22028, 22044, 23054, 24024, 24042, 14044])
 @pytest.mark.parametrize("G", [128, -1])
 def test_every_gemv_variant(variant, G, monkeypatch):
     """Each small-batch GEMV instantiation, with and without cross-workgroup
