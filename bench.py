@@ -8,36 +8,46 @@ uniform 0..15, scales uniform [0.002, 0.02]), fp16 activations ~N(0,1) at
 M = 1, 8 and 32.  One step runs the four linears at each of the three M
 values (12 GEMMs) on one of 36 distinct weight copies (1.9 GB in total, far
 past the 256 MB Infinity Cache), rotating copies from step to step; each step
-is one HIP-graph replay, as decode steps are replayed in SGLite.
+is one HIP-graph replay, as decode steps are replayed in SGLite, timed between
+its own pair of HIP events.
 
-value = algorithmic bytes of the timed steps / their time (GB/s), where one
+value = algorithmic bytes of one step / the median step time (GB/s), where one
 linear moves K*N/2 (int4) + (K/128)*N/2 (zeros) + (K/128)*N*2 (scales)
-+ 2*M*K (x) + 2*M*N (y) bytes.
++ 2*M*K (x) + 2*M*N (y) bytes (config.value_from_mean gives the mean-based
+figure).  Every other duration is also a median of >= 50 samples.
 
 Also reported on the same line:
   roofline      the dominant decode kernel of the step (the one with the most
-                time; ops.gemm_kernel names the kernel of each shape): algorithmic
+                time; ops.plan_info names the kernel of each shape): algorithmic
                 bytes of its launches / their durations, measured with HIP events
                 around graphs of back-to-back launches on the launch stream,
                 against 8 TB/s HBM; `traffic` is its HBM bytes per launch from
                 the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
-                calibrated on a copy of known size; --pmc-workload/--pmc-summary).
-  decode_kernels  the same figures for every decode kernel of the step.
-  per_m         the same per batch size.
-  prefill       Llama-3-8B's four linears at M = 2048, TFLOP/s against the
-                2.5 PFLOP/s dense fp16 MFMA peak (MFMA-bound regime).
-  stack70b      the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at M = 64
-                (GB/s) and M = 4096 (TFLOP/s), layer after layer.
-  cpu_baseline  the CPU oracle (dequantise + fp32 matmul + cast) on the host
-                cores for one pass of the layer at M = 1, 8, 32.
+                calibrated on a copy of known size; --pmc-workload/--pmc-summary);
+                `attainable_GB/s` / `frac_of_attainable` set it against the
+                streaming probe (awq_stream_probe) run with the same grid, block
+                and bytes: what a launch of that shape reaches with no arithmetic.
+  decode_kernels, per_m   the same per kernel and per batch size, with each
+                linear's probe ceiling (and the best ceiling over a few grids).
+  llama3_8b     config 2: Llama-3-8B's four linears at M = 1, 16, 256, 2048, 8192
+                (GB/s and fraction of HBM at decode sizes, TFLOP/s and fraction of
+                the 2.5 PFLOP/s dense fp16 MFMA peak from M = 256);
+  prefill       its M = 2048 aggregate (and M = 8192).
+  mlp           the Qwen3-4B gated MLP with the activation fused vs unfused.
+  moe           config 4: the Qwen3-30B-A3B-shaped grouped MoE forward.
+  stack70b      config 3: the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at
+                M = 64 (GB/s, one graph per pass) and M = 4096 (TFLOP/s).
+  cpu_baseline  the CPU oracle on the host cores for configs 0-4 (dequantisation
+                and matmul timed separately, 2 warm-ups, median of 5); value is
+                config 1 in GB/s.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Profiles (summaries committed under profiles/):
   rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --steps 500 \
-      --no-cpu-baseline --no-prefill --no-moe;  python3 bench.py --rocprof-summary decode <dir>
+      --no-cpu-baseline --no-prefill --no-moe --no-stack --no-mlp;  python3 bench.py --rocprof-summary decode <dir>
   rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --no-decode \
-      --no-moe --no-cpu-baseline;  python3 bench.py --rocprof-summary prefill <dir>
+      --no-moe --no-cpu-baseline --no-stack --no-mlp;  python3 bench.py --rocprof-summary prefill <dir>
   rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) ... -- python3 bench.py --pmc-workload;
       python3 bench.py --pmc-summary <fetch_dir> <write_dir>
 """
@@ -118,7 +128,7 @@ def stack70b_bench(ops, dev: torch.device, gen: torch.Generator) -> dict:
               for _ in range(STACK70B_LAYERS)]
     cnts = {name: ops.make_counters(N, dev) for name, K, N in STACK70B}
     res = {}
-    for M, passes in ((64, 5), (4096, 2)):
+    for M, passes in ((64, 20), (4096, 3)):
         xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.float16) for _, K, _ in STACK70B}
         outs = {name: torch.empty((M, N), dtype=torch.float16, device=dev) for name, _, N in STACK70B}
 
@@ -127,24 +137,27 @@ def stack70b_bench(ops, dev: torch.device, gen: torch.Generator) -> dict:
                 for name, K, N in STACK70B:
                     ops.gemm(xs[K], lay[name], K, N, G, counters=cnts[name], out=outs[name])
 
-        stack()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(passes):
+        if M <= 256:
+            # a batched decode step is replayed as one graph (cuda_graph.py:153-157)
+            g = graph_of(stack)
+            time_replays([g], 2)
+            ms = median(replay_samples([g], passes))
+            del g
+        else:
             stack()
-        b.record()
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / passes
+            ms = median(call_samples(stack, passes))
         byt = STACK70B_LAYERS * sum(gemm_bytes(M, N, K) for _, K, N in STACK70B)
         fl = STACK70B_LAYERS * sum(2 * M * N * K for _, K, N in STACK70B)
-        res[str(M)] = {"ms_per_pass": round(ms, 2), "GB/s": round(byt / ms / 1e6, 1),
-                       "TFLOP/s": round(fl / ms / 1e9, 1)}
+        res[str(M)] = {"ms_per_pass": round(ms, 2), "passes": passes, "GB/s": round(byt / ms / 1e6, 1),
+                       "frac_hbm": round(byt / ms / 1e6 / HBM_PEAK_GBS, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+                       "frac_mfma": round(fl / ms / 1e9 / MFMA_FP16_PEAK_TFLOPS, 4),
+                       "launch": "one HIP graph per pass" if M <= 256 else "eager, back to back"}
         del xs, outs
     del layers
     torch.cuda.synchronize()
     return {"workload": "Llama-3.1-70B-shaped AWQ stack, 80 x {qkv 8192x10240, o 8192x8192, gate_up 8192x57344, "
-                        "down 28672x8192}, int4 group 128 with zeros, fp16; layer-by-layer launches",
+                        "down 28672x8192}, int4 group 128 with zeros, fp16; layer-by-layer launches; median over "
+                        "the passes",
             "weight_bytes": STACK70B_LAYERS * sum(gemm_bytes(0, N, K) for _, K, N in STACK70B), "per_m": res}
 
 
@@ -161,7 +174,7 @@ def graph_of(fn) -> torch.cuda.CUDAGraph:
 
 
 def time_replays(graphs, n: int) -> float:
-    """ms for n replays cycling through graphs, HIP events on the current stream."""
+    """ms for n back-to-back replays cycling through graphs, HIP events on the current stream."""
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -173,7 +186,41 @@ def time_replays(graphs, n: int) -> float:
     return a.elapsed_time(b)
 
 
-def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, reps: int = 20) -> dict:
+def replay_samples(graphs, n: int) -> list:
+    """ms of each of n replays (cycling through graphs), each between its own pair of HIP events on
+    the launch stream; the replays still run back to back."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i in range(n):
+        graphs[i % len(graphs)].replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
+
+
+def call_samples(fn, n: int) -> list:
+    """ms of each of n eager calls of fn, between HIP events on the current stream."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    evs[0].record()
+    for i in range(n):
+        fn()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
+
+
+def median(v) -> float:
+    v = sorted(v)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+
+
+MEDIAN_SAMPLES = 60  # samples behind every median (>= 50)
+
+
+def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, reps: int = MEDIAN_SAMPLES) -> dict:
     """Qwen3-4B gated MLP block (gate_up 2560x19456 -> silu(gate) * up -> down 9728x2560)
     at M = 1, 8, 32: the activation fused into the gate_up GEMM's epilogue, against
     the same GEMMs with the activation as separate torch ops (the reference's
@@ -202,7 +249,8 @@ def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, re
         t = {}
         for name, fn in (("unfused", unfused), ("fused", fused)):
             g = graph_of(lambda: [fn(c) for c in range(copies)])
-            t[name] = time_replays([g], reps) * 1e3 / (reps * copies)
+            time_replays([g], 3)
+            t[name] = median(replay_samples([g], reps)) * 1e3 / copies
         res[str(M)] = {"fused_us": round(t["fused"], 2), "unfused_us": round(t["unfused"], 2),
                        "speedup": round(t["unfused"] / t["fused"], 3)}
     return {"workload": "Qwen3-4B gated MLP block: gate_up 2560x19456 + silu(gate)*up + down 9728x2560, int4 group "
@@ -210,7 +258,7 @@ def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, re
                         "between the GEMMs", "per_m": res}
 
 
-def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, reps: int = 50) -> dict:
+def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, reps: int = MEDIAN_SAMPLES) -> dict:
     """Qwen3-30B-A3B-shaped experts: E=128, H=2048, I=768, top-8 of softmax(N(0,1) logits), T=512.
 
     One forward = routing, alignment, grouped gate_up GEMM with silu_and_mul,
@@ -250,7 +298,7 @@ def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, rep
 
     graphs = [graph_of(forward(c)) for c in range(copies)]
     time_replays(graphs, 10)
-    us = time_replays(graphs, reps) * 1e3 / reps
+    us = median(replay_samples(graphs, reps)) * 1e3
 
     # Per-kernel durations: graphs of `copies` back-to-back launches of one stage.
     tw, ids = fused_topk(x, logits, k, True)
@@ -274,7 +322,7 @@ def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, rep
         n = copies if name in ("gate_up_silu", "down_routed") else 20
         g = graph_of(lambda fn=fn, n=n: [fn(c % copies) for c in range(n)])
         time_replays([g], 3)
-        kern[name] = round(time_replays([g], 10) * 1e3 / (10 * n), 2)
+        kern[name] = round(median(replay_samples([g], MEDIAN_SAMPLES)) * 1e3 / n, 2)
         del g
 
     def wbytes(K, N):
@@ -293,25 +341,112 @@ def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, rep
             "kernel": "moe_gemm_kernel (grouped W4A16)", "copies": copies}
 
 
-def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 30) -> dict:
-    """The CPU oracle on the same layer, repeated until about ``min_seconds`` of work."""
+def _host_cores() -> int:
+    """Cores this process may use: the affinity set, capped by OMP_NUM_THREADS when the host sets it
+    (a GPU box allots each GPU a share of its cores), never more than os.cpu_count()."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
+
+
+def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
+    """The CPU oracle on the host cores: the oracle's torch dequantisation
+    (unpack in AWQ nibble order, (q - z) * s rounded once; pinned bit for bit against the numpy
+    oracle) and fp32 matmul + cast, timed separately; `warmup` untimed runs, then the median of
+    `runs`.  Configs 0-2 in full except Llama-3-8B's M = 2048 and 8192, which time the o_proj
+    (4096x4096) alone; config 3 times one 70B-shaped o_proj (8192x8192) and scales it by the
+    layer's weight and flop counts (the full stack would need ~137 GB of fp16 weights); config 4
+    runs the expert loop over 16 of the 128 experts and scales by 8.  value = the headline
+    workload (config 1: Qwen3-4B layer at M = 1, 8, 32) in the metric's GB/s."""
     from oracle import awq_oracle as oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = _host_cores()
     torch.set_num_threads(threads)
-    total_b, total_t, passes = 0, 0.0, 0
-    warm = oracle.make_awq_linear(256, 256, G, seed=0)
-    oracle.awq_gemm(oracle.make_activation(1, 256, 0), warm["qweight"], warm["qzeros"], warm["scales"], None, G)
-    tensors = [oracle.make_awq_linear(K, N, G, seed=i) for i, (_, K, N) in enumerate(LAYER)]
-    xs = {(M, K): oracle.make_activation(M, K, seed=100 + M) for M in M_SET for _, K, _ in LAYER}
-    while passes < max_passes and (passes == 0 or total_t < min_seconds):
-        for t, (_, K, N) in zip(tensors, LAYER):
-            for M in M_SET:
-                t0 = time.perf_counter()
-                oracle.awq_gemm(xs[(M, K)], t["qweight"], t["qzeros"], t["scales"], None, G)
-                total_t += time.perf_counter() - t0
-                total_b += gemm_bytes(M, N, K)
-        passes += 1
+    t_start = time.perf_counter()
+
+    def med(fn):
+        for _ in range(warmup):
+            fn()
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return median(ts)
+
+    def linear_times(K, N, Ms, seed):
+        t = oracle.make_awq_linear(K, N, G, seed=seed)
+        box = {}
+        td = med(lambda: box.__setitem__("W", oracle.dequantize_torch(t["qweight"], t["qzeros"], t["scales"], G)))
+        Wf = box["W"].float()
+        tm = {}
+        for M in Ms:
+            x = oracle.make_activation(M, K, seed=100 + M).float()
+            tm[M] = med(lambda: (x @ Wf).to(torch.float16))
+        return td, tm
+
+    res = {}
+    # config 0: Qwen3-4B qkv at M = 16
+    td, tm = linear_times(2560, 6144, (16,), 0)
+    res["config0_qkv_m16"] = {"dequant_s": round(td, 4), "matmul_s": round(tm[16], 4),
+                              "GB/s": round(gemm_bytes(16, 6144, 2560) / (td + tm[16]) / 1e9, 3)}
+    # config 1: the Qwen3-4B layer at M = 1, 8, 32 (the headline workload)
+    step_b, step_t, deq_t, mm_t = 0, 0.0, 0.0, 0.0
+    for i, (_, K, N) in enumerate(LAYER):
+        td, tm = linear_times(K, N, M_SET, i)
+        for M in M_SET:
+            step_b += gemm_bytes(M, N, K)
+            step_t += td + tm[M]
+            mm_t += tm[M]
+        deq_t += td
+    res["config1_qwen3_4b_layer"] = {"dequant_s_per_layer": round(deq_t, 4), "matmul_s_per_step": round(mm_t, 4),
+                                     "GB/s": round(step_b / step_t / 1e9, 3)}
+    value = step_b / step_t / 1e9
+    # config 2: Llama-3-8B layer at M = 1, 16, 256 in full; 2048 and 8192 on the o_proj
+    per_m = {M: [0, 0, 0.0] for M in LLAMA_M}
+    for i, (name, K, N) in enumerate(PREFILL):
+        Ms = [M for M in LLAMA_M if M <= 256 or name == "o_proj"]
+        td, tm = linear_times(K, N, Ms, 10 + i)
+        for M in Ms:
+            per_m[M][0] += gemm_bytes(M, N, K)
+            per_m[M][1] += 2 * M * N * K
+            per_m[M][2] += td + tm[M]
+    res["config2_llama3_8b"] = {str(M): {"GB/s": round(b / t / 1e9, 3), "TFLOP/s": round(f / t / 1e12, 4)}
+                                for M, (b, f, t) in per_m.items()}
+    # config 3: one 70B-shaped o_proj, scaled to the 80-layer stack
+    K3, N3 = 8192, 8192
+    td, tm = linear_times(K3, N3, (64, 4096), 20)
+    w_layer = sum(K * N for _, K, N in STACK70B)
+    c3 = {}
+    for M in (64, 4096):
+        t_stack = 80 * (td + tm[M]) * w_layer / (K3 * N3)
+        c3[str(M)] = {"s_per_stack_estimate": round(t_stack, 2),
+                      "GB/s": round(80 * sum(gemm_bytes(M, N, K) for _, K, N in STACK70B) / t_stack / 1e9, 3),
+                      "TFLOP/s": round(80 * sum(2 * M * N * K for _, K, N in STACK70B) / t_stack / 1e12, 4)}
+    res["config3_70b_stack"] = c3
+    # config 4: expert loop (gate_up 2048->1536 + silu_and_mul + down 768->2048), 16 of 128 experts
+    E, Es, H, I, T, k = 128, 16, 2048, 768, 512, 8
+    ex = [(oracle.make_awq_linear(H, 2 * I, G, seed=30 + e), oracle.make_awq_linear(I, H, G, seed=300 + e))
+          for e in range(Es)]
+    rows = T * k // E  # routed rows per expert on average
+    xe = oracle.make_activation(rows, H, seed=5).float()
+
+    def experts():
+        for w1, w2 in ex:
+            W1 = oracle.dequantize_torch(w1["qweight"], w1["qzeros"], w1["scales"], G).float()
+            W2 = oracle.dequantize_torch(w2["qweight"], w2["qzeros"], w2["scales"], G).float()
+            h = (xe @ W1).to(torch.float16).float()
+            a = (h[:, :I] / (1.0 + torch.exp(-h[:, :I])) * h[:, I:]).to(torch.float16).float()
+            (a @ W2).to(torch.float16)
+    t4 = med(experts) * E / Es
+    wb = E * (gemm_bytes(0, 2 * I, H) + gemm_bytes(0, H, I))
+    res["config4_moe"] = {"s_estimate": round(t4, 3), "GB/s": round((wb + T * k * (H + 2 * I + I + H) * 2) / t4 / 1e9, 3)}
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -321,9 +456,12 @@ def cpu_baseline(min_seconds: float = 10.0, max_passes: int = 30) -> dict:
                     break
     except OSError:
         pass
-    return {"value": round(total_b / total_t / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": "CPU oracle (numpy unpack + dequantise, fp32 torch matmul, fp16 cast) over the same layer's "
-                      f"4 linears at M=1,8,32, {passes} passes ({total_t:.1f} s); host {model}"}
+    return {"value": round(value, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle (torch dequantise, pinned bit-exact to the numpy oracle, + fp32 matmul + fp16 "
+                      f"cast), {warmup} warm-ups then the median of {runs}; value = the Qwen3-4B layer at M = 1, 8, "
+                      f"32 (config 1); other configs in per_config ({time.perf_counter() - t_start:.1f} s in all); "
+                      f"host {model}, os.cpu_count() = {os.cpu_count()}",
+            "per_config": res}
 
 
 PMC_COPY_BYTES = 256 << 20
@@ -522,40 +660,82 @@ def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
     return "\n".join(lines) + "\n"
 
 
-def decode_bench(ops, args, C, linear, step_fn, step_bytes):
-    """The decode step: graph replays over the C weight copies, then
-    per-launch durations of every (M, linear) and the dominant kernel's
-    roofline figures."""
+PROBE_GRIDS = ((256, 256), (256, 1024), (512, 256), (1024, 256), (2048, 256))
+
+
+class Prober:
+    """The streaming probe (awq_stream_probe) over C distinct regions of one device buffer: per
+    launch shape and byte count, the median duration of one launch, from graphs of C back-to-back
+    launches (each region read once per graph, so nothing is served from the Infinity Cache)."""
+
+    def __init__(self, ops, dev, C: int, region_bytes: int):
+        self.ops, self.C, self.region = ops, C, (region_bytes + 4095) // 4096 * 4096
+        self.buf = torch.empty(C * self.region, dtype=torch.uint8, device=dev)
+        self.buf.fill_(7)
+        self.sink = torch.empty(1 << 16, dtype=torch.int32, device=dev)
+        self.cache = {}
+
+    def us(self, nbytes: int, grid: int, block: int) -> float:
+        nbytes = nbytes // 16 * 16
+        key = (nbytes, grid, block)
+        if key not in self.cache:
+            def f():
+                for c in range(self.C):
+                    self.ops.stream_probe(self.buf[c * self.region:], nbytes, grid, block, self.sink)
+            g = graph_of(f)
+            time_replays([g], 2)
+            self.cache[key] = median(replay_samples([g], MEDIAN_SAMPLES)) * 1e3 / self.C
+            del g
+        return self.cache[key]
+
+    def best(self, nbytes: int) -> tuple:
+        return min((self.us(nbytes, g, b), g, b) for g, b in PROBE_GRIDS)
+
+
+def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
+    """The decode step: `args.steps` timed graph replays over the C weight copies (each between its
+    own HIP events; value from the median), then the median per-launch duration of every
+    (M, linear), its attainable ceiling from the streaming probe at the same grid, block and bytes,
+    and the dominant kernel's roofline figures."""
     steps = [graph_of(step_fn(c)) for c in range(C)]
     time_replays(steps, args.warmup)
-    ms = time_replays(steps, args.steps)
-    ms_per_step = ms / args.steps
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    samples = replay_samples(steps, args.steps)
+    ms_med, ms_mean = median(samples), sum(samples) / len(samples)
     del steps
 
-    # Per-launch durations of the decode kernel: graphs of C back-to-back
-    # launches of one (M, linear) over the C weight copies.
+    # Per-launch durations: graphs of C back-to-back launches of one (M, linear)
+    # over the C weight copies, MEDIAN_SAMPLES replays.
     per_m, per_kernel = {}, {}
     for M in M_SET:
-        mb, mt, lin = 0, 0.0, {}
+        mb, mt, mp, lin = 0, 0.0, 0.0, {}
         for name, K, N in LAYER:
             def f(M=M, name=name, K=K, N=N):
                 for c in range(C):
                     linear(c, M, name, K, N)
             g = graph_of(f)
             time_replays([g], 2)
-            us = time_replays([g], 5) * 1e3 / (5 * C)
+            us = median(replay_samples([g], MEDIAN_SAMPLES)) * 1e3 / C
+            del g
             b = gemm_bytes(M, N, K)
-            kern = ops.gemm_kernel(M, N, K, G)
-            lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1), "kernel": kern}
-            acc = per_kernel.setdefault(kern, {"launches": 0, "bytes": 0, "us": 0.0})
+            info = ops.plan_info(M, N, K, G)
+            probe = prober.us(b, info.workgroups, info.threads)
+            best_us, best_g, best_b = prober.best(b)
+            kern = info.kernel
+            lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                         "kernel": kern, "grid": info.workgroups, "block": info.threads, "k_slices": info.k_slices,
+                         "ceiling_us": round(probe, 3), "frac_of_ceiling": round(probe / us, 4),
+                         "best_grid_ceiling_us": round(best_us, 3), "best_grid": [best_g, best_b]}
+            acc = per_kernel.setdefault(kern, {"launches": 0, "bytes": 0, "us": 0.0, "probe_us": 0.0})
             acc["launches"] += 1
             acc["bytes"] += b
             acc["us"] += us
+            acc["probe_us"] += probe
             mb += b
             mt += us
-            del g
-        per_m[str(M)] = {"GB/s": round(mb / mt / 1e3, 1), "us_per_layer": round(mt, 3), "linears": lin}
+            mp += probe
+        per_m[str(M)] = {"GB/s": round(mb / mt / 1e3, 1), "frac_hbm": round(mb / mt / 1e3 / HBM_PEAK_GBS, 4),
+                         "us_per_layer": round(mt, 3), "ceiling_us_per_layer": round(mp, 3),
+                         "frac_of_ceiling": round(mp / mt, 4), "linears": lin}
     # The dominant kernel is the one with the most time in the step.
     dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
     d = per_kernel[dom]
@@ -564,10 +744,68 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes):
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic(dom),
                 "kernel": dom, "launches_per_step": d["launches"],
                 "bytes_per_launch_avg": d["bytes"] // d["launches"],
-                "us_per_launch_avg": round(d["us"] / d["launches"], 3)}
+                "us_per_launch_avg": round(d["us"] / d["launches"], 3),
+                "attainable_GB/s": round(d["bytes"] / d["probe_us"] / 1e3, 1),
+                "frac_of_attainable": round(d["probe_us"] / d["us"], 4)}
     kernels = {k: {"launches_per_step": v["launches"], "GB/s": round(v["bytes"] / v["us"] / 1e3, 1),
-                   "us_per_step": round(v["us"], 3)} for k, v in per_kernel.items()}
-    return value, ms_per_step, roofline, kernels, per_m
+                   "us_per_step": round(v["us"], 3), "frac_of_ceiling": round(v["probe_us"] / v["us"], 4)}
+               for k, v in per_kernel.items()}
+    return {"value": step_bytes / (ms_med * 1e-3) / 1e9, "value_mean": step_bytes / (ms_mean * 1e-3) / 1e9,
+            "ms_per_step": ms_med, "ms_per_step_mean": ms_mean, "roofline": roofline, "kernels": kernels,
+            "per_m": per_m}
+
+
+LLAMA_M = (1, 16, 256, 2048, 8192)
+
+
+def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
+    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192), int4 group
+    128, fp16.  M <= 256: graphs of back-to-back launches over `copies` weight copies (1.1 GB);
+    M >= 2048: eager calls.  Median over MEDIAN_SAMPLES samples; GB/s against the HBM peak (and the
+    streaming probe's ceiling at decode sizes) and TFLOP/s against the dense fp16 MFMA peak."""
+    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in PREFILL} for _ in range(copies)]
+    cnts = {name: ops.make_counters(N, dev) for name, K, N in PREFILL}
+    xg = torch.Generator(device=dev).manual_seed(3)
+    res = {}
+    for M in LLAMA_M:
+        xs = {K: torch.randn((M, K), generator=xg, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
+        outs = {name: torch.empty((M, N), dtype=torch.float16, device=dev) for name, _, N in PREFILL}
+        lin, tb, tf, tt = {}, 0, 0, 0.0
+        for name, K, N in PREFILL:
+            def call(c, name=name, K=K, N=N):
+                ops.gemm(xs[K], reps[c][name], K, N, G, counters=cnts[name], out=outs[name])
+            if M <= 256:
+                g = graph_of(lambda: [call(c) for c in range(copies)])
+                time_replays([g], 2)
+                us = median(replay_samples([g], MEDIAN_SAMPLES)) * 1e3 / copies
+                del g
+            else:
+                for _ in range(3):
+                    call(0)
+                it = iter(range(10 ** 9))
+                us = median(call_samples(lambda: call(next(it) % copies), MEDIAN_SAMPLES)) * 1e3
+            b, fl = gemm_bytes(M, N, K), 2 * M * N * K
+            info = ops.plan_info(M, N, K, G)
+            e = {"us": round(us, 2), "GB/s": round(b / us / 1e3, 1), "TFLOP/s": round(fl / us / 1e6, 1),
+                 "kernel": info.kernel, "grid": info.workgroups, "k_slices": info.k_slices}
+            if M <= 32:
+                probe = prober.us(b, info.workgroups, info.threads)
+                e.update({"frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "ceiling_us": round(probe, 3),
+                          "frac_of_ceiling": round(probe / us, 4)})
+            else:
+                e["frac_mfma"] = round(fl / us / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)
+            lin[name] = e
+            tb, tf, tt = tb + b, tf + fl, tt + us
+        res[str(M)] = {"us_per_layer": round(tt, 2), "GB/s": round(tb / tt / 1e3, 1),
+                       "frac_hbm": round(tb / tt / 1e3 / HBM_PEAK_GBS, 4), "TFLOP/s": round(tf / tt / 1e6, 1),
+                       "frac_mfma": round(tf / tt / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4),
+                       "bound": "hbm" if M <= 32 else "mfma", "linears": lin}
+        del xs, outs
+    del reps
+    torch.cuda.synchronize()
+    return {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, down 14336x4096), "
+                        f"int4 group 128 with zeros, fp16, M in {list(LLAMA_M)}; {copies} weight copies; median of "
+                        f"{MEDIAN_SAMPLES}", "per_m": res}
 
 
 def main() -> int:
@@ -637,57 +875,55 @@ def main() -> int:
         return f
 
     step_bytes = sum(gemm_bytes(M, N, K) for M in M_SET for _, K, N in LAYER)
-    value, ms_per_step, roofline, kernels, per_m = None, None, None, None, None
+    # Region per probe launch: the largest decode linear's bytes (Qwen3-4B gate_up / Llama-3-8B gate_up).
+    prober = Prober(ops, dev, max(C, 10), max(gemm_bytes(32, N, K) for _, K, N in LAYER + PREFILL))
+    dec = None
     if C > 0:
-        value, ms_per_step, roofline, kernels, per_m = decode_bench(ops, args, C, linear, step_fn, step_bytes)
-
+        progress("decode step")
+        dec = decode_bench(ops, args, C, linear, step_fn, step_bytes, prober)
+    del reps
     torch.cuda.synchronize()
 
-    prefill = None
+    llama = None
     if not args.no_prefill:
-        M = PREFILL_M
-        x = {K: torch.randn((M, K), generator=xg, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
-        tot_f, tot_t, lin = 0, 0.0, {}
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for name, K, N in PREFILL:
-            r = make_repacked(ops, K, N, gen, dev)
-            cnt = ops.make_counters(N, dev)
-            out = torch.empty((M, N), dtype=torch.float16, device=dev)
-            for _ in range(3):
-                ops.gemm(x[K], r, K, N, G, counters=cnt, out=out)
-            torch.cuda.synchronize()
-            n = 10
-            a.record()
-            for _ in range(n):
-                ops.gemm(x[K], r, K, N, G, counters=cnt, out=out)
-            b.record()
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / n
-            fl = 2 * M * N * K
-            lin[name] = {"us": round(us, 1), "TFLOP/s": round(fl / us / 1e6, 1)}
-            tot_f += fl
-            tot_t += us
-            del r
-        tf = tot_f / tot_t / 1e6
+        progress("llama3-8b sweep")
+        llama = llama_bench(ops, dev, gen, prober)
+    del prober
+    torch.cuda.synchronize()
+    prefill = None
+    if llama is not None:
+        pm = llama["per_m"][str(PREFILL_M)]
         prefill = {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, "
-                               "down 14336x4096) at M=2048, fp16", "TFLOP/s": round(tf, 1),
-                   "peak": MFMA_FP16_PEAK_TFLOPS, "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4),
-                   "kernel": "tiled_kernel", "linears": lin}
+                               f"down 14336x4096) at M={PREFILL_M}, fp16", "TFLOP/s": pm["TFLOP/s"],
+                   "peak": MFMA_FP16_PEAK_TFLOPS, "frac": pm["frac_mfma"], "kernel": "tiled_kernel",
+                   "linears": {k: {"us": v["us"], "TFLOP/s": v["TFLOP/s"]} for k, v in pm["linears"].items()},
+                   "m8192": {"TFLOP/s": llama["per_m"]["8192"]["TFLOP/s"],
+                             "frac": llama["per_m"]["8192"]["frac_mfma"]}}
 
-    mlp = None if args.no_mlp else mlp_bench(ops, dev, gen)
-    moe = None if args.no_moe else moe_bench(ops, dev, gen)
-    stack = None if args.no_stack else stack70b_bench(ops, dev, gen)
+    mlp = moe = stack = None
+    if not args.no_mlp:
+        progress("gated mlp")
+        mlp = mlp_bench(ops, dev, gen)
+    if not args.no_moe:
+        progress("moe")
+        moe = moe_bench(ops, dev, gen)
+    if not args.no_stack:
+        progress("70b stack")
+        stack = stack70b_bench(ops, dev, gen)
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    cpu = None
+    if not args.no_cpu_baseline:
+        progress("cpu baseline")
+        cpu = cpu_baseline()
 
     line = {
         "metric": METRIC,
-        "value": None if value is None else round(value, 1),
+        "value": None if dec is None else round(dec["value"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": None if ms_per_step is None else round(ms_per_step, 5),
+        "ms_per_step": None if dec is None else round(dec["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -695,20 +931,28 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "Qwen3-4B decoder layer AWQ linears (qkv 2560x6144, o_proj 4096x2560, "
                                "gate_up 2560x19456, down 9728x2560), int4 group 128 with zero points, fp16 "
-                               "scales/activations, M in {1, 8, 32} per step, HIP-graph replay",
+                               "scales/activations, M in {1, 8, 32} per step, HIP-graph replay; value and "
+                               "ms_per_step from the median of the timed steps",
                    "weight_copies": C, "weight_bytes_rotated": C * sum(gemm_bytes(0, N, K) for _, K, N in LAYER),
-                   "step_bytes": step_bytes},
-        "roofline": roofline,
-        "decode_kernels": kernels,
-        "per_m": per_m,
+                   "step_bytes": step_bytes,
+                   "value_from_mean": None if dec is None else round(dec["value_mean"], 1),
+                   "ms_per_step_mean": None if dec is None else round(dec["ms_per_step_mean"], 5)},
+        "roofline": None if dec is None else dec["roofline"],
+        "cpu_baseline": cpu,
+        "decode_kernels": None if dec is None else dec["kernels"],
+        "per_m": None if dec is None else dec["per_m"],
         "prefill": prefill,
+        "llama3_8b": llama,
         "mlp": mlp,
         "moe": moe,
         "stack70b": stack,
-        "cpu_baseline": cpu,
     }
     print(json.dumps(line))
     return 0
+
+
+def progress(what: str) -> None:
+    print(f"[bench] {what} ({time.strftime('%H:%M:%S')})", file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":

@@ -81,8 +81,13 @@ int awq_unrepack_cdna4(const void* w, const void* s, const void* z, int dtype, i
 int awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype,
                 int64_t K, int64_t N, int64_t G, void* w_out, awq_stream_t stream);
 
-/* Same result from the repacked buffers, computed by the device routine the
- * GEMM kernels use (proves the in-kernel dequantisation is bit-exact). */
+/* Same result from the repacked buffers, computed by Dq<>::word, the
+ * dequantisation routine of the prefill kernel (tiled_kernel), the grouped
+ * MoE kernel and the bf16 GEMV path (proves their in-kernel dequantisation is
+ * bit-exact).  The fp16 decode paths feed the MFMAs the exact integers q - z
+ * (GEMV, 4+ rows) or the biased nibbles 1024 + q (GEMV up to 3 rows and the
+ * skinny kernel) and apply the group scale to the fp32 sums instead; their
+ * outputs are checked against the oracle within the GEMM tolerance. */
 int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype, int64_t K, int64_t N,
                          int64_t G, void* w_out, awq_stream_t stream);
 
@@ -94,10 +99,12 @@ int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype,
  * (python/sglite/srt/model_executor/layers/quantization/marlin_utils.py:388-415).
  *
  * Split-K scratch: `ws` must hold awq_workspace_bytes(M, N, K, G) bytes (any
- * content; may be NULL when that is 0).  `counters` must hold
- * awq_counter_bytes(N) bytes that are zero before the first call on them;
- * every call leaves them zero again.  Calls sharing `counters` must not run
- * concurrently (use one counters buffer per stream). */
+ * content; may be NULL when that is 0).  `counters` (int32, counter_bytes
+ * long) must hold at least awq_counter_bytes(N) bytes that are zero before the
+ * first call on them; every call leaves them zero again.  Both are checked
+ * whenever the plan splits K (AWQ_STATUS_WORKSPACE if missing or short).
+ * Calls sharing `counters` must not run concurrently (use one counters
+ * buffer per stream). */
 int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G);
 /* Which kernel awq_w4a16_gemm runs for this shape: 0 = decode split-K kernel,
  * 1 = tiled MFMA kernel, 2 = small-batch GEMV kernel (benchmarks and
@@ -106,7 +113,7 @@ int awq_gemm_kernel_kind(int64_t M, int64_t N, int64_t K, int64_t G);
 int64_t awq_counter_bytes(int64_t N);
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype,
-                   void* ws, int64_t ws_bytes, int32_t* counters, awq_stream_t stream);
+                   void* ws, int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream);
 
 /* ---- W4A16 GEMM with the gated activation fused ----------------------------
  * out[M, N/2] = act(gate) * up, where [gate | up] = x[M, K] @ W (+ bias[N]) are
@@ -127,7 +134,57 @@ int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G);
 int awq_gemm_kernel_kind_act(int64_t M, int64_t N, int64_t K, int64_t G);
 int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
-                       int64_t ws_bytes, int32_t* counters, awq_stream_t stream);
+                       int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream);
+
+/* ---- planner overrides (tests and sweeps) -----------------------------------
+ * Force a kernel choice or split for every later GEMM of the process (all
+ * threads), e.g. to run each kernel instantiation against the oracle.  The
+ * planner's own choice is best for serving; the overrides are off by default
+ * and never read from the environment.  Shape codes that are not
+ * instantiated are ignored.  No counterpart in the reference.
+ *   AWQ_PLAN_GEMV_MAX_M      largest M routed to the GEMV kernel (0 disables it)
+ *   AWQ_PLAN_GEMV_VARIANT    GEMV shape ntw*10000 + wn*1000 + wk*10 + kpw
+ *   AWQ_PLAN_GEMV_KS         GEMV k-slices across workgroups
+ *   AWQ_PLAN_SKINNY_VARIANT  decode-kernel shape ntw*10000 + wn*100 + wk
+ *   AWQ_PLAN_SKINNY_KS       decode-kernel k-slices
+ *   AWQ_PLAN_TILED_MIN_M     smallest M routed to the tiled kernel
+ *   AWQ_PLAN_TILED_BM        tiled row block (32, 64 or 128)
+ *   AWQ_PLAN_TILED_KS        tiled k-slices                                   */
+enum {
+  AWQ_PLAN_GEMV_MAX_M = 0,
+  AWQ_PLAN_GEMV_VARIANT = 1,
+  AWQ_PLAN_GEMV_KS = 2,
+  AWQ_PLAN_SKINNY_VARIANT = 3,
+  AWQ_PLAN_SKINNY_KS = 4,
+  AWQ_PLAN_TILED_MIN_M = 5,
+  AWQ_PLAN_TILED_BM = 6,
+  AWQ_PLAN_TILED_KS = 7
+};
+int awq_set_plan_override(int knob, int value);
+void awq_clear_plan_overrides(void);
+
+/* Compute units of the current device that the planner fills (queried once
+ * per device; 256 when no device is visible).  No counterpart in the
+ * reference. */
+int awq_device_cu_count(void);
+
+/* ---- diagnostics and measurement (no counterpart in the reference) ---------
+ * awq_gemm_plan_info: the plan that awq_w4a16_gemm (activation 0) or
+ * awq_w4a16_gemm_act (AWQ_ACT_SILU / AWQ_ACT_GELU) runs for this shape on the
+ * current device, written to info[0..5]: kernel kind (as
+ * awq_gemm_kernel_kind), shape code, k-slices across workgroups, workgroups
+ * per launch, threads per workgroup, workspace bytes.
+ *
+ * awq_stream_probe: streams `bytes` (a multiple of 16, src 16-byte aligned)
+ * with `grid` workgroups of `block` threads (64..1024, a multiple of 64),
+ * every thread issuing all its 16-byte loads before consuming them, and
+ * stores one word per workgroup to sink (sink_bytes >= 4 * grid).  Timed with
+ * a GEMM's own grid and block size and its weight bytes, it gives the rate a
+ * launch of that shape can reach at all (the decode roofline's attainable
+ * ceiling). */
+int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activation, int64_t* info);
+int awq_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink, int64_t sink_bytes,
+                     awq_stream_t stream);
 
 /* ---- grouped MoE -------------------------------------------------------------
  * The stages of the fused MoE backend

@@ -131,6 +131,34 @@ def dequantize(qweight, qzeros, scales: torch.Tensor, group_size: Optional[int] 
     return torch.from_numpy(w64).to(scales.dtype)
 
 
+def dequantize_torch(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor,
+                     group_size: Optional[int] = None) -> torch.Tensor:
+    """:func:`dequantize` in multithreaded CPU torch (the CPU baseline's dequantisation).
+
+    Same arithmetic: the nibble of logical column 8j + i is
+    (word >> 4 * REVERSE_AWQ_ORDER[i]) & 0xF, q - z is an exact integer, and
+    its product with the scale is exact in fp32 (a 4-bit by an 11- or 8-bit
+    significand), so converting the fp32 product is the one rounding.  Pinned
+    bit for bit against :func:`dequantize` in tests/test_oracle.py.
+    """
+    K, N8 = qweight.shape
+    N = N8 * 8
+    if group_size is None:
+        group_size = K // qzeros.shape[0]
+    G = resolve_group_size(group_size, K)
+    shifts = torch.tensor([4 * o for o in REVERSE_AWQ_ORDER], dtype=torch.int32)
+
+    def unpack(p: torch.Tensor) -> torch.Tensor:
+        return ((p.unsqueeze(-1) >> shifts) & 0xF).reshape(p.shape[0], N)
+
+    q = unpack(qweight.cpu()).to(torch.float32)
+    z = unpack(qzeros.cpu()).to(torch.float32)
+    s = scales.cpu().to(torch.float32)
+    q = q.view(K // G, G, N)
+    q.sub_(z.unsqueeze(1)).mul_(s.unsqueeze(1))
+    return q.view(K, N).to(scales.dtype)
+
+
 def awq_gemm(x: torch.Tensor, qweight, qzeros, scales: torch.Tensor, bias: Optional[torch.Tensor] = None,
              group_size: Optional[int] = None) -> torch.Tensor:
     """fp32-accumulated AWQ linear: y = rnd(x @ W) (+ bias in the activation dtype).
@@ -406,6 +434,46 @@ def make_awq_linear(K: int, N: int, group_size: int = 128, seed: int = 0,
 def make_activation(M: int, K: int, seed: int, dtype: torch.dtype = torch.float16) -> torch.Tensor:
     g = torch.Generator().manual_seed(seed)
     return torch.randn((M, K), generator=g).to(dtype)
+
+
+ADVERSARIAL_KINDS = ("mean10", "outliers", "near_max")
+
+
+def make_adversarial_activation(M: int, K: int, kind: str, seed: int,
+                                dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Activations that stress the fp32 accumulation of the decode kernels:
+
+    * ``mean10``: N(10, 1), a large common mean (sum_k x grows like 10 K);
+    * ``outliers``: N(0, 1) with 1% of the channels scaled by 300 and two
+      channels at +-1000 (the outlier channels AWQ's scales are chosen for);
+    * ``near_max``: N(0, 1) with two channels at +-5e4 (fp16 near its maximum;
+      with |W| <= 0.3 the outputs stay finite).
+    The outlier channels are the same for every row."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((M, K), generator=g)
+    ch = torch.randperm(K, generator=g)
+    if kind == "mean10":
+        x = x + 10.0
+    elif kind == "outliers":
+        x[:, ch[:max(1, K // 100)]] *= 300.0
+        x[:, ch[K // 100]] = 1000.0
+        x[:, ch[K // 100 + 1]] = -1000.0
+    elif kind == "near_max":
+        x[:, ch[0]] = 5.0e4
+        x[:, ch[1]] = -5.0e4
+    else:
+        raise ValueError(f"unknown activation kind {kind!r}")
+    return x.to(dtype)
+
+
+def elementwise_ok(out: torch.Tensor, ref: torch.Tensor, rtol: float, atol_frac: float) -> Tuple[bool, float]:
+    """|out - ref| <= rtol * |ref| + atol_frac * max|ref| for every element; also the worst ratio of
+    the error to that bound (<= 1 passes)."""
+    o = out.detach().cpu().float()
+    r = ref.detach().cpu().float()
+    bound = rtol * r.abs() + atol_frac * float(r.abs().max())
+    ratio = float(((o - r).abs() / bound.clamp_min(1e-30)).max()) if o.numel() else 0.0
+    return bool(torch.isfinite(o).all()) and ratio <= 1.0, ratio
 
 
 def tolerance_ok(out: torch.Tensor, ref: torch.Tensor, rel: float = 2e-2) -> Tuple[bool, float, float]:

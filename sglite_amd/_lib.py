@@ -41,11 +41,17 @@ SIGNATURES = {
     "awq_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "awq_counter_bytes": (_i64, [_i64]),
     "awq_gemm_kernel_kind": (_int, [_i64, _i64, _i64, _i64]),
-    "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp]),
+    "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
+                              _vp]),
     "awq_workspace_bytes_act": (_i64, [_i64, _i64, _i64, _i64]),
     "awq_gemm_kernel_kind_act": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm_act": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp,
-                                  _vp]),
+                                  _i64, _vp]),
+    "awq_set_plan_override": (_int, [_int, _int]),
+    "awq_clear_plan_overrides": (None, []),
+    "awq_device_cu_count": (_int, []),
+    "awq_gemm_plan_info": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_i64)]),
+    "awq_stream_probe": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _vp]),
     "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i64)]),
     "awq_moe_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),
@@ -59,6 +65,15 @@ SIGNATURES = {
 
 AWQ_ACT_SILU = 1
 AWQ_ACT_GELU = 2
+
+AWQ_PLAN_GEMV_MAX_M = 0
+AWQ_PLAN_GEMV_VARIANT = 1
+AWQ_PLAN_GEMV_KS = 2
+AWQ_PLAN_SKINNY_VARIANT = 3
+AWQ_PLAN_SKINNY_KS = 4
+AWQ_PLAN_TILED_MIN_M = 5
+AWQ_PLAN_TILED_BM = 6
+AWQ_PLAN_TILED_KS = 7
 
 AWQ_MOE_ACT_NONE = 0
 AWQ_MOE_ACT_SILU = 1

@@ -71,6 +71,41 @@ int check_shape(int64_t K, int64_t N, int64_t G, int dtype, int64_t* G_out) {
   return AWQ_STATUS_OK;
 }
 
+// Split-K arrival counters: the GEMV and decode kernels index one int32 per
+// column tile (awq_counter_bytes); the tiled kernel reduces in a second
+// kernel and needs none.
+int check_counters(const GemmPlan& p, int64_t N, const int32_t* counters, int64_t counter_bytes, const char* who) {
+  if (p.kind == 1) return AWQ_STATUS_OK;
+  const int64_t need = ((N + 15) / 16) * 4;
+  if (!counters) return fail(AWQ_STATUS_WORKSPACE, "%s: split-K needs the counters buffer", who);
+  if (counter_bytes < need)
+    return fail(AWQ_STATUS_WORKSPACE, "%s: counters of %lld bytes needed, %lld given", who, (long long)need,
+                (long long)counter_bytes);
+  if (!aligned(counters, 4)) return fail(AWQ_STATUS_WORKSPACE, "%s: counters must be 4-byte aligned", who);
+  return AWQ_STATUS_OK;
+}
+
+// Arguments of a plain GEMM call, checked; on success (and M > 0) the
+// geometry and plan.
+int gemm_prepare(const void* x, const void* w, const void* s, const void* z, const void* bias, const void* out,
+                 int64_t M, int64_t N, int64_t K, int64_t G, int dtype, const char* who, Geom* g, GemmPlan* p) {
+  int64_t Gr = 0;
+  int st = check_shape(K, N, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative, got %lld", (long long)M);
+  if (M == 0) return ok();
+  if (M > (int64_t(1) << 24)) return fail(AWQ_STATUS_UNSUPPORTED, "M must be below 2^24, got %lld", (long long)M);
+  if (!x || !w || !s || !z || !out) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: null pointer argument", who);
+  if (!aligned(x, 16)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: x must be 16-byte aligned", who);
+  if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: out must be 8-byte aligned", who);
+  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: repacked buffers must be 16-byte aligned", who);
+  if (bias && !aligned(bias, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: bias must be 8-byte aligned", who);
+  *g = make_geom(M, N, K, Gr);
+  *p = plan_gemm(*g);
+  return AWQ_STATUS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -177,29 +212,18 @@ int64_t awq_counter_bytes(int64_t N) {
 
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype, void* ws, int64_t ws_bytes,
-                   int32_t* counters, awq_stream_t stream) {
-  int64_t Gr = 0;
-  int st = check_shape(K, N, G, dtype, &Gr);
-  if (st != 0) return st;
-  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative, got %lld", (long long)M);
-  if (M == 0) return ok();
-  if (M > (int64_t(1) << 24)) return fail(AWQ_STATUS_UNSUPPORTED, "M must be below 2^24, got %lld", (long long)M);
-  if (!x || !w || !s || !z || !out)
-    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: null pointer argument");
-  if (!aligned(x, 16)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: x must be 16-byte aligned");
-  if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: out must be 8-byte aligned");
-  if (!aligned(w, 16) || !aligned(s, 16) || !aligned(z, 16))
-    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: repacked buffers must be 16-byte aligned");
-  if (bias && !aligned(bias, 8))
-    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_w4a16_gemm: bias must be 8-byte aligned");
-  const Geom g = make_geom(M, N, K, Gr);
-  const GemmPlan p = plan_gemm(g);
+                   int32_t* counters, int64_t counter_bytes, awq_stream_t stream) {
+  Geom g;
+  GemmPlan p;
+  int st = gemm_prepare(x, w, s, z, bias, out, M, N, K, G, dtype, "awq_w4a16_gemm", &g, &p);
+  if (st != 0 || M == 0) return st;
   if (p.ws_bytes > 0) {
     if (!ws || ws_bytes < p.ws_bytes)
       return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: workspace of %lld bytes needed, %lld given",
                   (long long)p.ws_bytes, (long long)(ws ? ws_bytes : 0));
     if (!aligned(ws, 16)) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: workspace must be 16-byte aligned");
-    if (!counters) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm: split-K needs the counters buffer");
+    st = check_counters(p, N, counters, counter_bytes, "awq_w4a16_gemm");
+    if (st != 0) return st;
   }
   return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
                     "awq_w4a16_gemm launch");
@@ -228,7 +252,7 @@ int awq_gemm_kernel_kind_act(int64_t M, int64_t N, int64_t K, int64_t G) {
 
 int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
-                       int64_t ws_bytes, int32_t* counters, awq_stream_t stream) {
+                       int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream) {
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -258,10 +282,59 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
       return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: workspace of %lld bytes needed, %lld given",
                   (long long)p.ws_bytes, (long long)(ws ? ws_bytes : 0));
     if (!aligned(ws, 16)) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: workspace must be 16-byte aligned");
-    if (!counters) return fail(AWQ_STATUS_WORKSPACE, "awq_w4a16_gemm_act: split-K needs the counters buffer");
+    const int st2 = check_counters(p, N, counters, counter_bytes, "awq_w4a16_gemm_act");
+    if (st2 != 0) return st2;
   }
   return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, act, (hipStream_t)stream),
                     "awq_w4a16_gemm_act launch");
+}
+
+int awq_set_plan_override(int knob, int value) {
+  if (!set_plan_override(knob, value))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_set_plan_override: unknown knob %d", knob);
+  return ok();
+}
+
+void awq_clear_plan_overrides(void) { clear_plan_overrides(); }
+
+int awq_device_cu_count(void) { return device_cu_count(); }
+
+int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activation, int64_t* info) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_gemm_plan_info: M must be positive");
+  if (activation != 0 && activation != AWQ_ACT_SILU && activation != AWQ_ACT_GELU)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_gemm_plan_info: unknown activation %d", activation);
+  if (activation != 0 && N % 32 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "a gate/up projection needs N %% 32 == 0, got %lld", (long long)N);
+  if (!info) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_gemm_plan_info: null pointer argument");
+  const GemmPlan p = plan_gemm(make_geom(M, N, K, Gr), activation == 0 ? kActNone : kActSilu);
+  info[0] = p.kind;
+  info[1] = p.variant;
+  info[2] = p.ks;
+  info[3] = p.grid_x * p.grid_y * (p.kind == 1 ? p.ks : 1);
+  info[4] = plan_threads(p);
+  info[5] = p.ws_bytes;
+  return ok();
+}
+
+int awq_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink, int64_t sink_bytes,
+                     awq_stream_t stream) {
+  if (bytes <= 0 || bytes % 16 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: bytes must be a positive multiple of 16");
+  if (grid <= 0 || grid >= (int64_t(1) << 31))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: grid must be in [1, 2^31)");
+  if (block < 64 || block > 1024 || block % 64 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: block must be a multiple of 64 in [64, 1024]");
+  if (!src || !sink) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: null pointer argument");
+  if (!aligned(src, 16) || !aligned(sink, 4))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: src must be 16-byte and sink 4-byte aligned");
+  if (sink_bytes < 4 * grid)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_stream_probe: sink of %lld bytes needed, %lld given",
+                (long long)(4 * grid), (long long)sink_bytes);
+  return hip_status(launch_stream_probe(src, bytes, grid, block, sink, (hipStream_t)stream),
+                    "awq_stream_probe launch");
 }
 
 int64_t awq_moe_sorted_capacity(int64_t numel, int64_t E, int64_t block_size) {

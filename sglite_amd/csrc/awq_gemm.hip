@@ -12,9 +12,10 @@
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
 // and gptq_marlin_gemm (marlin_utils.py:388-410).
-#include <stdlib.h>
+#include <limits.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "awq_device.h"
@@ -28,12 +29,19 @@ namespace {
 // ---------------------------------------------------------------------------
 // Planning and dispatch.
 // ---------------------------------------------------------------------------
-constexpr int kNumCU = 256;
+// Planner overrides (tests and sweeps only; see awq_set_plan_override).  An
+// unset knob holds kUnset and the planner's own choice stands.
+constexpr int kUnset = INT_MIN;
+std::atomic<int> g_override[kPlanKnobs] = {kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset};
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return (v && *v) ? atoi(v) : dflt;
+int knob(int k, int dflt) {
+  const int v = g_override[k].load(std::memory_order_relaxed);
+  return v == kUnset ? dflt : v;
 }
+
+// CU count of each device, queried once (0 = not yet known).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
 
 // Decode-kernel shapes that are instantiated (ntw * 10000 + wn * 100 + wk).
 bool skinny_variant_ok(int v) {
@@ -77,6 +85,40 @@ int64_t gemv_min_ks(const Geom& g, int v) {
   return (g.KT + (int64_t)wk * kpw - 1) / ((int64_t)wk * kpw);
 }
 }  // namespace
+
+bool set_plan_override(int k, int value) {
+  if (k < 0 || k >= kPlanKnobs) return false;
+  g_override[k].store(value, std::memory_order_relaxed);
+  return true;
+}
+
+void clear_plan_overrides() {
+  for (auto& o : g_override) o.store(kUnset, std::memory_order_relaxed);
+}
+
+// Compute units of the current device (what the grid and split-K choices fill),
+// from hipDeviceAttributeMultiprocessorCount on the first call per device; a
+// partitioned MI355X (CPX/DPX modes) reports its partition's share.  256 (a
+// whole MI355X) when no device is visible, so that host-only planning queries
+// stay answerable.
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (dev < kMaxDevices) {
+    const int c = g_cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  if (dev < kMaxDevices) g_cus[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 // GEMV variant (code ntw * 10000 + wn * 1000 + wk * 10 + kpw): 8 waves of at
 // most 3 or 4 k-tiles each, whichever splits K fewer times (3 on a tie: fewer
@@ -134,7 +176,7 @@ int gemv_default_variant(const Geom& g, int act) {
 // A fused gate/up activation keeps the GEMV kernel up to 4 rows, and up to 8
 // rows when K fits in 24 k-tiles.
 bool gemv_preferred(const Geom& g, int act) {
-  const int forced = env_int("SGL_AWQ_GEMV_MAX_M", -1);
+  const int forced = knob(kPlanGemvMaxM, -1);
   if (forced >= 0) return g.M <= forced;
   if (act) return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
   if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
@@ -148,11 +190,11 @@ bool gemv_preferred(const Geom& g, int act) {
 bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
   if (g.NG > 1 && g.G < 128) return false;
   int v = gemv_default_variant(g, act);
-  const int env = env_int("SGL_AWQ_GEMV_VARIANT", 0);
+  const int env = knob(kPlanGemvVariant, 0);
   if (gemv_variant_ok(env) && (!act || env / 10000 == 2)) v = env;
   if (!gemv_variant_ok(v)) return false;
   const int ntw = v / 10000, wn = (v / 1000) % 10;
-  const int env_ks = env_int("SGL_AWQ_GEMV_KS", 0);
+  const int env_ks = knob(kPlanGemvKs, 0);
   const GemvSplit sp = gemv_split(g, v, env_ks > 0 ? env_ks : gemv_min_ks(g, v));
   if (sp.ks == 0) return false;
   p.kind = 2;
@@ -181,7 +223,7 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
 //  * 14-16 rows on gate_up-sized matrices (N >= 16384, K * N >= 20M).
 // A fused gate/up activation uses the 17-32 and 14-16 row rules only.
 bool tiled_preferred(const Geom& g, int act) {
-  const int forced = env_int("SGL_AWQ_TILED_MIN_M", 0);
+  const int forced = knob(kPlanTiledMinM, 0);
   if (forced > 0) return g.M >= forced;
   if (g.M > 32) return true;
   const int64_t kn = g.K * g.N;
@@ -221,7 +263,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
       wn = 2;
       wk = g.M <= 16 ? 4 : 2;
     }
-    const int env = env_int("SGL_AWQ_SKINNY_VARIANT", 0);
+    const int env = knob(kPlanSkinnyVariant, 0);
     if (skinny_variant_ok(env) && (!act || env / 10000 == 2)) {
       ntw = env / 10000;
       wn = (env / 100) % 100;
@@ -231,15 +273,15 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     p.variant = ntw * 10000 + wn * 100 + wk;
     p.grid_x = (g.NT + ntg - 1) / ntg;
     int64_t ks = 1;
-    if (p.grid_x < kNumCU / 2) {
+    if (p.grid_x < g.cus / 2) {
       // Few column tiles: split K so about one workgroup per CU is busy,
       // keeping >= 4 k-tiles per wave and the partial traffic
       // (KS * M * N * 8 bytes) below a quarter of the weight stream.
-      ks = (kNumCU + p.grid_x - 1) / p.grid_x;
+      ks = (g.cus + p.grid_x - 1) / p.grid_x;
       ks = std::min(ks, std::max<int64_t>(1, g.KT / (2 * wk)));
       ks = std::min(ks, std::max<int64_t>(1, g.K / (64 * g.M)));
     }
-    const int env_ks = env_int("SGL_AWQ_SKINNY_KS", 0);
+    const int env_ks = knob(kPlanSkinnyKs, 0);
     if (env_ks > 0) ks = env_ks;
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
     p.ktc = (int)((g.KT + ks - 1) / ks);
@@ -254,9 +296,9 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 256 workgroups x (k-tiles per slice + 1), a 64-row step costing 0.75
     // and a 32-row step 0.3 of a 128-row one, plus the partial traffic of the
     // split-K reduction.  The 32-row block serves batches of at most 32 rows.
-    const int env_bm = env_int("SGL_AWQ_TILED_BM", 0);
+    const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128;
-    const int env_ks = env_int("SGL_AWQ_TILED_KS", 0);
+    const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
@@ -268,7 +310,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
         if (env_ks > 0 ? ks != 1 : (ks > 1 && ks > g.KT / min_ktc)) continue;
         const int64_t ktc = (g.KT + ks - 1) / ks, kse = (g.KT + ktc - 1) / ktc;
         if (kse > 1 && kse * g.M * Np * 4 >= (int64_t(1) << 31)) continue;  // 32-bit partial offsets
-        const int64_t waves = (tiles * kse + kNumCU - 1) / kNumCU;
+        const int64_t waves = (tiles * kse + g.cus - 1) / g.cus;
         double t = (double)waves * (double)(ktc + 1) * (bm == 32 ? 0.3 : (bm == 64 ? 0.75 : 1.0));
         if (kse > 1) t += (double)kse * (double)g.M * (double)Np * 4.0 / 3.2e6;
         if (best_bm == 0 || t < best) {
@@ -290,6 +332,12 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
   }
   return p;
+}
+
+int plan_threads(const GemmPlan& p) {
+  if (p.kind == 1) return 256;
+  if (p.kind == 2) return 64 * ((p.variant / 1000) % 10) * ((p.variant / 10) % 100);
+  return 64 * ((p.variant / 100) % 100) * (p.variant % 100);
 }
 
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,

@@ -10,9 +10,28 @@ struct Geom {
   int64_t M, N, K, G;  // G already resolved (-1 -> K)
   int64_t NT, KT, NG;  // column tiles, row tiles, groups
   int gshift;          // group of row k = k >> gshift (31 for one group)
+  int cus;             // compute units the plan fills (device_cu_count())
 };
 
 Geom make_geom(int64_t M, int64_t N, int64_t K, int64_t G);
+
+// Compute units of the current device (256 when none is visible).
+int device_cu_count();
+
+// Planner overrides for tests and sweeps (awq_set_plan_override in the C ABI).
+enum : int {
+  kPlanGemvMaxM = 0,      // largest M routed to the GEMV kernel (0 disables it)
+  kPlanGemvVariant = 1,   // GEMV shape code ntw*10000 + wn*1000 + wk*10 + kpw
+  kPlanGemvKs = 2,        // GEMV k-slices
+  kPlanSkinnyVariant = 3, // decode-kernel shape code ntw*10000 + wn*100 + wk
+  kPlanSkinnyKs = 4,      // decode-kernel k-slices
+  kPlanTiledMinM = 5,     // smallest M routed to the tiled kernel
+  kPlanTiledBm = 6,       // tiled row block (32, 64, 128)
+  kPlanTiledKs = 7,       // tiled k-slices
+  kPlanKnobs = 8
+};
+bool set_plan_override(int knob, int value);
+void clear_plan_overrides();
 
 hipError_t launch_repack(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype,
                          const Geom& g, void* w_out, void* s_out, void* z_out, hipStream_t s);
@@ -82,6 +101,12 @@ struct MoeGemmParams {
   int dtype;
 };
 hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s);
+// Streaming probe (awq_probe.hip).
+hipError_t launch_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink,
+                               hipStream_t s);
+// Threads per workgroup of a plan's main kernel.
+int plan_threads(const GemmPlan& p);
+
 hipError_t launch_moe_sum(const void* in, void* out, int64_t T, int64_t k, int64_t H, int dtype, hipStream_t s);
 
 }  // namespace sgl_awq

@@ -166,6 +166,7 @@ Geom make_geom(int64_t M, int64_t N, int64_t K, int64_t G) {
   g.KT = (K + 127) / 128;
   g.NG = K / g.G;
   g.gshift = 31;
+  g.cus = M > 0 ? device_cu_count() : 256;
   if (g.NG > 1) {
     int s = 0;
     while ((int64_t(1) << s) < g.G) ++s;

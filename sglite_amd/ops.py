@@ -1,21 +1,33 @@
-"""Torch-facing wrappers over the C ABI.
+"""Torch custom ops over the C ABI (namespace ``torch.ops.sglite_awq``).
 
 PyTorch supplies device memory and the current HIP stream; all arithmetic runs
-in the HIP kernels of libsglite_awq.so.  Every function launches on
-``torch.cuda.current_stream()`` of the tensors' device, never synchronises and
-allocates only through torch's caching allocator, so it can be captured in a
-``torch.cuda.graph``.
+in the HIP kernels of libsglite_awq.so.  Every C-ABI entry point that launches
+work is registered with ``torch.library.custom_op`` and a fake (meta)
+implementation, so the ops are visible to ``torch.ops``, FakeTensor shape
+propagation and ``torch.compile``; this replaces the reference's dispatch
+through its torch ops ``sgl_kernel.gptq_marlin_gemm`` and
+``sgl_kernel.awq_marlin_repack``
+(python/sglite/srt/model_executor/layers/quantization/marlin_utils.py:388-410,
+awq_marlin.py:300-305).
+
+Every op launches on ``torch.cuda.current_stream()`` of its tensors' device,
+never synchronises and allocates only through torch's caching allocator, so
+it can be captured in a ``torch.cuda.graph``.  The plain-Python functions
+below (``gemm``, ``repack`` ...) are the wrappers the linear methods call;
+they validate arguments and call the registered ops.
 """
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
-from typing import NamedTuple, Optional, Tuple
+from typing import Dict, Iterator, List, NamedTuple, Optional, Tuple
 
 import torch
 
 from . import _lib
 
+NAMESPACE = "sglite_awq"
 _DTYPE_CODE = {torch.float16: _lib.AWQ_DTYPE_FP16, torch.bfloat16: _lib.AWQ_DTYPE_BF16}
 SUPPORTED_GROUP_SIZES = (-1, 32, 64, 128)
 
@@ -35,7 +47,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _require_cuda(*ts: torch.Tensor) -> None:
+def _require_cuda(*ts: Optional[torch.Tensor]) -> None:
     for t in ts:
         if t is not None and not t.is_cuda:
             raise ValueError("AWQ HIP kernels need device tensors")
@@ -46,6 +58,16 @@ def _aligned(t: torch.Tensor, a: int = 16) -> torch.Tensor:
     if t.is_contiguous() and t.data_ptr() % a == 0:
         return t
     return t.clone(memory_format=torch.contiguous_format)
+
+
+@contextlib.contextmanager
+def _on_device(device: torch.device) -> Iterator[None]:
+    """Make ``device`` current for the C ABI's planning (it fills that device's CUs)."""
+    if device.index is None or torch.cuda.current_device() == device.index:
+        yield
+    else:
+        with torch.cuda.device(device):
+            yield
 
 
 def resolve_group_size(group_size: int, K: int) -> int:
@@ -85,9 +107,13 @@ def _check_awq_shapes(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch
     return K, N, G
 
 
-def repack(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> Repacked:
-    """AWQ checkpoint tensors -> CDNA4 tile layout (device side, no host copy)."""
-    _require_cuda(qweight, qzeros, scales)
+# ---------------------------------------------------------------------------
+# Registered ops: repack / unrepack / dequantisation probes.
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_repack_cdna4", mutates_args=(), device_types="cuda")
+def _repack_op(qweight: torch.Tensor, qzeros: torch.Tensor,
+               scales: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     K, N, G = _check_awq_shapes(qweight, qzeros, scales)
     code = dtype_code(scales.dtype)
     wb, sb, zb = repacked_sizes(K, N, G)
@@ -98,53 +124,111 @@ def repack(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) ->
     z = torch.empty((NT, NG), dtype=torch.int64, device=dev)
     assert s.numel() * 2 == sb and z.numel() * 8 == zb
     qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
-    lib = _lib.load()
-    _lib.check(lib.awq_repack_cdna4(qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), code, K, N, G,
-                                    w.data_ptr(), s.data_ptr(), z.data_ptr(), _stream(dev)), "awq_repack_cdna4")
-    return Repacked(w, s, z)
+    with _on_device(dev):
+        _lib.check(_lib.load().awq_repack_cdna4(qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), code, K, N,
+                                                G, w.data_ptr(), s.data_ptr(), z.data_ptr(), _stream(dev)),
+                   "awq_repack_cdna4")
+    return w, s, z
+
+
+@_repack_op.register_fake
+def _(qweight, qzeros, scales):
+    K, N8 = qweight.shape
+    N, NG = N8 * 8, qzeros.shape[0]
+    NT, KT = (N + 15) // 16, (K + 127) // 128
+    return (qweight.new_empty(NT * KT * 256), scales.new_empty((NT, NG, 16)),
+            qweight.new_empty((NT, NG), dtype=torch.int64))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_unrepack_cdna4", mutates_args=(), device_types="cuda")
+def _unrepack_op(w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, K: int, N: int,
+                 G: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dev = w.device
+    qweight = torch.empty((K, N // 8), dtype=torch.int32, device=dev)
+    qzeros = torch.empty((K // G, N // 8), dtype=torch.int32, device=dev)
+    scales = torch.empty((K // G, N), dtype=s.dtype, device=dev)
+    with _on_device(dev):
+        _lib.check(_lib.load().awq_unrepack_cdna4(w.data_ptr(), s.data_ptr(), z.data_ptr(), dtype_code(s.dtype), K, N,
+                                                  G, qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr(),
+                                                  _stream(dev)), "awq_unrepack_cdna4")
+    return qweight, qzeros, scales
+
+
+@_unrepack_op.register_fake
+def _(w, s, z, K, N, G):
+    return (w.new_empty((K, N // 8)), w.new_empty((K // G, N // 8)), s.new_empty((K // G, N)))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_dequant", mutates_args=(), device_types="cuda")
+def _dequant_op(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    K, N, G = _check_awq_shapes(qweight, qzeros, scales)
+    out = torch.empty((K, N), dtype=scales.dtype, device=qweight.device)
+    with _on_device(qweight.device):
+        _lib.check(_lib.load().awq_dequant(qweight.contiguous().data_ptr(), qzeros.contiguous().data_ptr(),
+                                           scales.contiguous().data_ptr(), dtype_code(scales.dtype), K, N, G,
+                                           out.data_ptr(), _stream(qweight.device)), "awq_dequant")
+    return out
+
+
+@_dequant_op.register_fake
+def _(qweight, qzeros, scales):
+    return scales.new_empty((qweight.shape[0], qweight.shape[1] * 8))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_dequant_repacked", mutates_args=(), device_types="cuda")
+def _dequant_repacked_op(w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, K: int, N: int, G: int) -> torch.Tensor:
+    out = torch.empty((K, N), dtype=s.dtype, device=w.device)
+    with _on_device(w.device):
+        _lib.check(_lib.load().awq_dequant_repacked(w.data_ptr(), s.data_ptr(), z.data_ptr(), dtype_code(s.dtype), K,
+                                                    N, G, out.data_ptr(), _stream(w.device)), "awq_dequant_repacked")
+    return out
+
+
+@_dequant_repacked_op.register_fake
+def _(w, s, z, K, N, G):
+    return s.new_empty((K, N))
+
+
+def repack(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> Repacked:
+    """AWQ checkpoint tensors -> CDNA4 tile layout (device side, no host copy)."""
+    _require_cuda(qweight, qzeros, scales)
+    _check_awq_shapes(qweight, qzeros, scales)
+    dtype_code(scales.dtype)
+    return Repacked(*torch.ops.sglite_awq.awq_repack_cdna4(qweight, qzeros, scales))
 
 
 def unrepack(r: Repacked, K: int, N: int, group_size: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """CDNA4 tile layout -> AWQ (qweight, qzeros, scales)."""
     _require_cuda(r.w, r.s, r.z)
-    G = resolve_group_size(group_size, K)
-    dev = r.w.device
-    qweight = torch.empty((K, N // 8), dtype=torch.int32, device=dev)
-    qzeros = torch.empty((K // G, N // 8), dtype=torch.int32, device=dev)
-    scales = torch.empty((K // G, N), dtype=r.s.dtype, device=dev)
-    lib = _lib.load()
-    _lib.check(lib.awq_unrepack_cdna4(r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), dtype_code(r.s.dtype), K, N, G,
-                                      qweight.data_ptr(), qzeros.data_ptr(), scales.data_ptr(), _stream(dev)),
-               "awq_unrepack_cdna4")
-    return qweight, qzeros, scales
+    return tuple(torch.ops.sglite_awq.awq_unrepack_cdna4(r.w, r.s, r.z, K, N, resolve_group_size(group_size, K)))
 
 
 def dequant(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
     """W[K, N] = rnd((q - z) * s) from AWQ tensors (bit-exact probe)."""
     _require_cuda(qweight, qzeros, scales)
-    K, N, G = _check_awq_shapes(qweight, qzeros, scales)
-    out = torch.empty((K, N), dtype=scales.dtype, device=qweight.device)
-    lib = _lib.load()
-    _lib.check(lib.awq_dequant(qweight.contiguous().data_ptr(), qzeros.contiguous().data_ptr(),
-                               scales.contiguous().data_ptr(), dtype_code(scales.dtype), K, N, G, out.data_ptr(),
-                               _stream(qweight.device)), "awq_dequant")
-    return out
+    _check_awq_shapes(qweight, qzeros, scales)
+    return torch.ops.sglite_awq.awq_dequant(qweight, qzeros, scales)
 
 
 def dequant_repacked(r: Repacked, K: int, N: int, group_size: int) -> torch.Tensor:
-    """W[K, N] from the repacked tensors, via the GEMM kernels' dequant routine."""
+    """W[K, N] from the repacked tensors, via Dq<>::word (the prefill and MoE kernels' dequant routine)."""
     _require_cuda(r.w, r.s, r.z)
-    G = resolve_group_size(group_size, K)
-    out = torch.empty((K, N), dtype=r.s.dtype, device=r.w.device)
-    lib = _lib.load()
-    _lib.check(lib.awq_dequant_repacked(r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), dtype_code(r.s.dtype), K, N,
-                                        G, out.data_ptr(), _stream(r.w.device)), "awq_dequant_repacked")
-    return out
+    return torch.ops.sglite_awq.awq_dequant_repacked(r.w, r.s, r.z, K, N, resolve_group_size(group_size, K))
 
+
+# ---------------------------------------------------------------------------
+# Planning queries and overrides.
+# ---------------------------------------------------------------------------
 
 def workspace_bytes(M: int, N: int, K: int, group_size: int) -> int:
     G = resolve_group_size(group_size, K)
     return _lib.check(_lib.load().awq_workspace_bytes(M, N, K, G), "awq_workspace_bytes")
+
+
+def workspace_bytes_act(M: int, N: int, K: int, group_size: int) -> int:
+    """Split-K workspace of ``gemm(..., activation=...)`` (its plan pairs gate and up tiles)."""
+    G = resolve_group_size(group_size, K)
+    return _lib.check(_lib.load().awq_workspace_bytes_act(M, N, K, G), "awq_workspace_bytes_act")
 
 
 KERNEL_NAMES = {0: "skinny_kernel", 1: "tiled_kernel", 2: "gemv_kernel"}
@@ -160,19 +244,183 @@ def gemm_kernel(M: int, N: int, K: int, group_size: int, activation: Optional[st
     return KERNEL_NAMES[_lib.check(lib.awq_gemm_kernel_kind_act(M, N, K, G), "awq_gemm_kernel_kind_act")]
 
 
+class PlanInfo(NamedTuple):
+    kernel: str
+    variant: int
+    k_slices: int
+    workgroups: int
+    threads: int
+    workspace_bytes: int
+
+
+def plan_info(M: int, N: int, K: int, group_size: int, activation: Optional[str] = None) -> PlanInfo:
+    """The plan ``gemm`` runs for this shape on the current device."""
+    G = resolve_group_size(group_size, K)
+    info = (ctypes.c_int64 * 6)()
+    act = 0 if activation is None else _GATED_ACT[activation]
+    _lib.check(_lib.load().awq_gemm_plan_info(M, N, K, G, act, info), "awq_gemm_plan_info")
+    return PlanInfo(KERNEL_NAMES[int(info[0])], *[int(v) for v in info[1:]])
+
+
+PLAN_KNOBS = {"gemv_max_m": _lib.AWQ_PLAN_GEMV_MAX_M, "gemv_variant": _lib.AWQ_PLAN_GEMV_VARIANT,
+              "gemv_ks": _lib.AWQ_PLAN_GEMV_KS, "skinny_variant": _lib.AWQ_PLAN_SKINNY_VARIANT,
+              "skinny_ks": _lib.AWQ_PLAN_SKINNY_KS, "tiled_min_m": _lib.AWQ_PLAN_TILED_MIN_M,
+              "tiled_bm": _lib.AWQ_PLAN_TILED_BM, "tiled_ks": _lib.AWQ_PLAN_TILED_KS}
+
+
+def set_plan_override(knob: str, value: int) -> None:
+    """Force a planner choice for every later GEMM of the process (tests and sweeps)."""
+    _lib.check(_lib.load().awq_set_plan_override(PLAN_KNOBS[knob], int(value)), "awq_set_plan_override")
+
+
+def clear_plan_overrides() -> None:
+    _lib.load().awq_clear_plan_overrides()
+
+
+@contextlib.contextmanager
+def plan_overrides(**knobs: int) -> Iterator[None]:
+    """``with plan_overrides(gemv_max_m=0, skinny_variant=10104): ...`` -- all overrides are cleared on exit."""
+    try:
+        for k, v in knobs.items():
+            set_plan_override(k, v)
+        yield
+    finally:
+        clear_plan_overrides()
+
+
+def device_cu_count() -> int:
+    return int(_lib.load().awq_device_cu_count())
+
+
 def make_counters(N: int, device: torch.device) -> torch.Tensor:
     """Split-K arrival counters: zeroed once here, left zeroed by every GEMM call."""
     nbytes = _lib.check(_lib.load().awq_counter_bytes(N), "awq_counter_bytes")
     return torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
 
 
-def workspace_bytes_act(M: int, N: int, K: int, group_size: int) -> int:
-    """Split-K workspace of ``gemm(..., activation=...)`` (its plan pairs gate and up tiles)."""
-    G = resolve_group_size(group_size, K)
-    return _lib.check(_lib.load().awq_workspace_bytes_act(M, N, K, G), "awq_workspace_bytes_act")
+# ---------------------------------------------------------------------------
+# Split-K workspace: one growing buffer per (device, stream) for eager calls
+# (the reference sizes its Marlin workspace once at load, awq_marlin.py:298);
+# a call being captured into a graph takes a fresh buffer from the graph's
+# pool instead, so that replays never share eager memory.
+# ---------------------------------------------------------------------------
+
+_WS_CACHE: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(nbytes: int, device: torch.device) -> Optional[torch.Tensor]:
+    if nbytes <= 0:
+        return None
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), _stream(device))
+    buf = _WS_CACHE.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = buf
+    return buf
 
 
 _GATED_ACT = {"silu": _lib.AWQ_ACT_SILU, "gelu": _lib.AWQ_ACT_GELU}
+
+
+def _gemm_launch(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bias: Optional[torch.Tensor],
+                 counters: Optional[torch.Tensor], out: torch.Tensor, K: int, N: int, G: int, act: int) -> None:
+    M = x.shape[0]
+    if M == 0:
+        return
+    dev = x.device
+    lib = _lib.load()
+    with _on_device(dev):
+        if act == 0:
+            wsb = _lib.check(lib.awq_workspace_bytes(M, N, K, G), "awq_workspace_bytes")
+        else:
+            wsb = _lib.check(lib.awq_workspace_bytes_act(M, N, K, G), "awq_workspace_bytes_act")
+        ws = _workspace(wsb, dev)
+        cb = 0 if counters is None else counters.numel() * 4
+        if act == 0:
+            _lib.check(lib.awq_w4a16_gemm(x.data_ptr(), w.data_ptr(), s.data_ptr(), z.data_ptr(), _ptr(bias),
+                                          out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _ptr(ws), wsb,
+                                          _ptr(counters), cb, _stream(dev)), "awq_w4a16_gemm")
+        else:
+            _lib.check(lib.awq_w4a16_gemm_act(x.data_ptr(), w.data_ptr(), s.data_ptr(), z.data_ptr(), _ptr(bias),
+                                              out.data_ptr(), M, N, K, G, dtype_code(x.dtype), act, _ptr(ws), wsb,
+                                              _ptr(counters), cb, _stream(dev)), "awq_w4a16_gemm_act")
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_w4a16_gemm", mutates_args=("counters",), device_types="cuda")
+def _gemm_op(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bias: Optional[torch.Tensor],
+             counters: Optional[torch.Tensor], K: int, N: int, G: int) -> torch.Tensor:
+    out = torch.empty((x.shape[0], N), dtype=x.dtype, device=x.device)
+    _gemm_launch(x, w, s, z, bias, counters, out, K, N, G, 0)
+    return out
+
+
+@_gemm_op.register_fake
+def _(x, w, s, z, bias, counters, K, N, G):
+    return x.new_empty((x.shape[0], N))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_w4a16_gemm_out", mutates_args=("counters", "out"), device_types="cuda")
+def _gemm_out_op(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bias: Optional[torch.Tensor],
+                 counters: Optional[torch.Tensor], out: torch.Tensor, K: int, N: int, G: int) -> None:
+    _gemm_launch(x, w, s, z, bias, counters, out, K, N, G, 0)
+
+
+@_gemm_out_op.register_fake
+def _(x, w, s, z, bias, counters, out, K, N, G):
+    return None
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_w4a16_gemm_act", mutates_args=("counters",), device_types="cuda")
+def _gemm_act_op(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bias: Optional[torch.Tensor],
+                 counters: Optional[torch.Tensor], K: int, N: int, G: int, activation: str) -> torch.Tensor:
+    out = torch.empty((x.shape[0], N // 2), dtype=x.dtype, device=x.device)
+    _gemm_launch(x, w, s, z, bias, counters, out, K, N, G, _GATED_ACT[activation])
+    return out
+
+
+@_gemm_act_op.register_fake
+def _(x, w, s, z, bias, counters, K, N, G, activation):
+    return x.new_empty((x.shape[0], N // 2))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_w4a16_gemm_act_out", mutates_args=("counters", "out"),
+                         device_types="cuda")
+def _gemm_act_out_op(x: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, bias: Optional[torch.Tensor],
+                     counters: Optional[torch.Tensor], out: torch.Tensor, K: int, N: int, G: int,
+                     activation: str) -> None:
+    _gemm_launch(x, w, s, z, bias, counters, out, K, N, G, _GATED_ACT[activation])
+
+
+@_gemm_act_out_op.register_fake
+def _(x, w, s, z, bias, counters, out, K, N, G, activation):
+    return None
+
+
+def _check_out(out: torch.Tensor, shape: Tuple[int, ...], dtype: torch.dtype, device: torch.device,
+               what: str = "out") -> None:
+    if tuple(out.shape) != tuple(shape):
+        raise ValueError(f"{what} must have shape {tuple(shape)}, got {tuple(out.shape)}")
+    if out.dtype != dtype:
+        raise ValueError(f"{what} must be {dtype}, got {out.dtype}")
+    if out.device != device:
+        raise ValueError(f"{what} must be on {device}, got {out.device}")
+    if not out.is_contiguous() or out.data_ptr() % 8:
+        raise ValueError(f"{what} must be contiguous and 8-byte aligned")
+
+
+def _check_counters(counters: torch.Tensor, N: int, device: torch.device) -> None:
+    if counters.dtype != torch.int32:
+        raise ValueError(f"counters must be int32, got {counters.dtype}")
+    if counters.device != device:
+        raise ValueError(f"counters must be on {device}, got {counters.device}")
+    if not counters.is_contiguous():
+        raise ValueError("counters must be contiguous")
+    need = (N + 15) // 16
+    if counters.numel() < need:
+        raise ValueError(f"counters must hold at least {need} int32 (awq_counter_bytes({N}) bytes), "
+                         f"got {counters.numel()}")
 
 
 def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Optional[torch.Tensor] = None,
@@ -183,14 +431,17 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
     With ``activation`` ("silu" or "gelu") the two column halves of W are a
     merged gate/up projection and the output is ``act(gate) * up``, [M, N / 2],
     each half rounded (bias added) as the plain GEMM stores it, then the
-    product in fp32, rounded once."""
-    _require_cuda(x, r.w)
+    product in fp32, rounded once.  ``counters`` (from ``make_counters``, zero
+    between calls) is needed whenever the plan splits K across workgroups."""
+    _require_cuda(x, r.w, r.s, r.z)
     if x.dim() != 2 or x.shape[1] != K:
         raise ValueError(f"x must be [M, {K}], got {tuple(x.shape)}")
     if x.dtype != r.s.dtype:
         raise ValueError(f"activation dtype {x.dtype} does not match the scale dtype {r.s.dtype}")
     if activation is not None and activation not in _GATED_ACT:
         raise ValueError(f"unsupported activation {activation!r}")
+    if r.w.device != x.device or r.s.device != x.device or r.z.device != x.device:
+        raise ValueError("x and the repacked weights must be on one device")
     G = resolve_group_size(group_size, K)
     M = x.shape[0]
     dev = x.device
@@ -200,26 +451,35 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
         if bias.numel() != N:
             raise ValueError(f"bias must have {N} elements, got {bias.numel()}")
         bias = _aligned(bias.to(x.dtype).reshape(-1), 8)
-    ncols = N if activation is None else N // 2
-    if out is None:
-        out = torch.empty((M, ncols), dtype=x.dtype, device=dev)
-    lib = _lib.load()
-    if M > 0:
+    if counters is not None:
+        _check_counters(counters, N, dev)
+    elif M > 0:
         wsb = workspace_bytes(M, N, K, G) if activation is None else workspace_bytes_act(M, N, K, G)
-    else:
-        wsb = 0
-    ws = torch.empty(wsb, dtype=torch.uint8, device=dev) if wsb > 0 else None
-    if wsb > 0 and counters is None:
-        raise ValueError("this shape splits K across workgroups: pass the layer's counters (make_counters)")
+        if wsb > 0 and plan_info(M, N, K, G, activation).kernel != "tiled_kernel":
+            raise ValueError("this shape splits K across workgroups: pass the layer's counters (make_counters)")
+    ncols = N if activation is None else N // 2
+    if out is not None:
+        _check_out(out, (M, ncols), x.dtype, dev)
     if activation is None:
-        _lib.check(lib.awq_w4a16_gemm(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
-                                      out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _ptr(ws), wsb, _ptr(counters),
-                                      _stream(dev)), "awq_w4a16_gemm")
-    else:
-        _lib.check(lib.awq_w4a16_gemm_act(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), _ptr(bias),
-                                          out.data_ptr(), M, N, K, G, dtype_code(x.dtype), _GATED_ACT[activation],
-                                          _ptr(ws), wsb, _ptr(counters), _stream(dev)), "awq_w4a16_gemm_act")
+        if out is None:
+            return torch.ops.sglite_awq.awq_w4a16_gemm(x, r.w, r.s, r.z, bias, counters, K, N, G)
+        torch.ops.sglite_awq.awq_w4a16_gemm_out(x, r.w, r.s, r.z, bias, counters, out, K, N, G)
+        return out
+    if out is None:
+        return torch.ops.sglite_awq.awq_w4a16_gemm_act(x, r.w, r.s, r.z, bias, counters, K, N, G, activation)
+    torch.ops.sglite_awq.awq_w4a16_gemm_act_out(x, r.w, r.s, r.z, bias, counters, out, K, N, G, activation)
     return out
+
+
+def stream_probe(src: torch.Tensor, nbytes: int, grid: int, block: int, sink: torch.Tensor) -> None:
+    """Stream ``nbytes`` of ``src`` with ``grid`` workgroups of ``block`` threads (awq_stream_probe)."""
+    _require_cuda(src, sink)
+    if nbytes > src.numel() * src.element_size():
+        raise ValueError("nbytes exceeds the source buffer")
+    with _on_device(src.device):
+        _lib.check(_lib.load().awq_stream_probe(src.data_ptr(), nbytes, grid, block, sink.data_ptr(),
+                                                sink.numel() * sink.element_size(), _stream(src.device)),
+                   "awq_stream_probe")
 
 
 # ---------------------------------------------------------------------------
@@ -251,6 +511,40 @@ def expert_strides(K: int, N: int, group_size: int) -> Tuple[int, int, int]:
     return w.value, s.value, z.value
 
 
+@torch.library.custom_op(f"{NAMESPACE}::awq_repack_experts", mutates_args=(), device_types="cuda")
+def _repack_experts_op(qweight: torch.Tensor, qzeros: torch.Tensor,
+                       scales: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    E = qweight.shape[0]
+    K, N, G = _check_awq_shapes(qweight[0], qzeros[0], scales[0])
+    code = dtype_code(scales.dtype)
+    ws, ss, zs = expert_strides(K, N, G)
+    dev = qweight.device
+    w = torch.empty((E, ws // 4), dtype=torch.int32, device=dev)
+    s = torch.zeros((E, ss // 2), dtype=scales.dtype, device=dev)
+    z = torch.zeros((E, zs // 8), dtype=torch.int64, device=dev)
+    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
+    lib = _lib.load()
+    with _on_device(dev):
+        st = _stream(dev)
+        for e in range(E):
+            _lib.check(lib.awq_repack_cdna4(qweight[e].data_ptr(), qzeros[e].data_ptr(), scales[e].data_ptr(), code, K,
+                                            N, G, w[e].data_ptr(), s[e].data_ptr(), z[e].data_ptr(), st),
+                       "awq_repack_cdna4")
+    return w, s, z
+
+
+@_repack_experts_op.register_fake
+def _(qweight, qzeros, scales):
+    E, K, N8 = qweight.shape
+    N, NG = N8 * 8, qzeros.shape[1]
+    NT, KT = (N + 15) // 16, (K + 127) // 128
+
+    def up(b):
+        return (b + 255) // 256 * 256
+    return (qweight.new_empty((E, up(NT * KT * 1024) // 4)), scales.new_empty((E, up(NT * NG * 32) // 2)),
+            qweight.new_empty((E, up(NT * NG * 8) // 8), dtype=torch.int64))
+
+
 def repack_experts(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Tensor) -> RepackedExperts:
     """AWQ expert stacks ``[E, K, N/8]`` / ``[E, K/G, N/8]`` / ``[E, K/G, N]`` -> stacked tile layout.
 
@@ -263,19 +557,29 @@ def repack_experts(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.Te
     if qzeros.shape[0] != E or scales.shape[0] != E:
         raise ValueError("qweight, qzeros and scales must stack the same number of experts")
     K, N, G = _check_awq_shapes(qweight[0], qzeros[0], scales[0])
-    code = dtype_code(scales.dtype)
-    ws, ss, zs = expert_strides(K, N, G)
-    dev = qweight.device
-    w = torch.empty((E, ws // 4), dtype=torch.int32, device=dev)
-    s = torch.zeros((E, ss // 2), dtype=scales.dtype, device=dev)
-    z = torch.zeros((E, zs // 8), dtype=torch.int64, device=dev)
-    qweight, qzeros, scales = qweight.contiguous(), qzeros.contiguous(), scales.contiguous()
-    lib = _lib.load()
-    st = _stream(dev)
-    for e in range(E):
-        _lib.check(lib.awq_repack_cdna4(qweight[e].data_ptr(), qzeros[e].data_ptr(), scales[e].data_ptr(), code, K, N, G,
-                                        w[e].data_ptr(), s[e].data_ptr(), z[e].data_ptr(), st), "awq_repack_cdna4")
+    dtype_code(scales.dtype)
+    w, s, z = torch.ops.sglite_awq.awq_repack_experts(qweight, qzeros, scales)
     return RepackedExperts(w, s, z, K, N, G)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_moe_topk_softmax", mutates_args=(), device_types="cuda")
+def _topk_op(gating_output: torch.Tensor, topk: int, renormalize: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    logits = _aligned(gating_output.float(), 4)
+    T, E = logits.shape
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    with _on_device(logits.device):
+        _lib.check(_lib.load().awq_moe_topk_softmax(logits.data_ptr(), w.data_ptr(), ids.data_ptr(), T, E, topk,
+                                                    1 if renormalize else 0, _stream(logits.device)),
+                   "awq_moe_topk_softmax")
+    return w, ids
+
+
+@_topk_op.register_fake
+def _(gating_output, topk, renormalize):
+    T = gating_output.shape[0]
+    return (gating_output.new_empty((T, topk), dtype=torch.float32),
+            gating_output.new_empty((T, topk), dtype=torch.int32))
 
 
 def moe_topk_softmax(gating_output: torch.Tensor, topk: int, renormalize: bool) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -283,14 +587,7 @@ def moe_topk_softmax(gating_output: torch.Tensor, topk: int, renormalize: bool) 
     _require_cuda(gating_output)
     if gating_output.dim() != 2:
         raise ValueError("gating_output must be [T, E]")
-    logits = _aligned(gating_output.float(), 4)
-    T, E = logits.shape
-    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
-    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
-    _lib.check(_lib.load().awq_moe_topk_softmax(logits.data_ptr(), w.data_ptr(), ids.data_ptr(), T, E, topk,
-                                                1 if renormalize else 0, _stream(logits.device)),
-               "awq_moe_topk_softmax")
-    return w, ids
+    return tuple(torch.ops.sglite_awq.awq_moe_topk_softmax(gating_output, topk, bool(renormalize)))
 
 
 class MoeAlignment(NamedTuple):
@@ -300,28 +597,67 @@ class MoeAlignment(NamedTuple):
     expert_offsets: torch.Tensor      # int32 [E + 1]
 
 
-def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int) -> MoeAlignment:
-    """Stable sort of the routed rows by expert, buckets padded to ``block_size`` (sentinel ``topk_ids.numel()``)."""
-    _require_cuda(topk_ids)
-    if topk_ids.dtype != torch.int32:
-        raise ValueError("topk_ids must be int32")
-    ids = topk_ids.contiguous().reshape(-1)
-    n = ids.numel()
+def _align_caps(n: int, num_experts: int, block_size: int) -> Tuple[int, int]:
     lib = _lib.load()
     cap = _lib.check(lib.awq_moe_sorted_capacity(n, num_experts, block_size), "awq_moe_sorted_capacity")
     bcap = _lib.check(lib.awq_moe_block_capacity(n, num_experts, block_size), "awq_moe_block_capacity")
+    return cap, bcap
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_moe_align_block_size", mutates_args=(), device_types="cuda")
+def _align_op(topk_ids: torch.Tensor, block_size: int,
+              num_experts: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    ids = topk_ids.contiguous().reshape(-1)
+    n = ids.numel()
+    cap, bcap = _align_caps(n, num_experts, block_size)
     dev = ids.device
     sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
     expert_ids = torch.empty(bcap, dtype=torch.int32, device=dev)
     npp = torch.empty(1, dtype=torch.int32, device=dev)
     offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
-    _lib.check(lib.awq_moe_align_block_size(ids.data_ptr() if n else None, n, num_experts, block_size,
-                                            sorted_ids.data_ptr(), expert_ids.data_ptr(), npp.data_ptr(),
-                                            offsets.data_ptr(), _stream(dev)), "awq_moe_align_block_size")
-    return MoeAlignment(sorted_ids, expert_ids, npp, offsets)
+    with _on_device(dev):
+        _lib.check(_lib.load().awq_moe_align_block_size(ids.data_ptr() if n else None, n, num_experts, block_size,
+                                                        sorted_ids.data_ptr(), expert_ids.data_ptr(), npp.data_ptr(),
+                                                        offsets.data_ptr(), _stream(dev)), "awq_moe_align_block_size")
+    return sorted_ids, expert_ids, npp, offsets
+
+
+@_align_op.register_fake
+def _(topk_ids, block_size, num_experts):
+    cap, bcap = _align_caps(topk_ids.numel(), num_experts, block_size)
+    return (topk_ids.new_empty(cap), topk_ids.new_empty(bcap), topk_ids.new_empty(1),
+            topk_ids.new_empty(num_experts + 1))
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int) -> MoeAlignment:
+    """Stable sort of the routed rows by expert, buckets padded to ``block_size`` (sentinel ``topk_ids.numel()``)."""
+    _require_cuda(topk_ids)
+    if topk_ids.dtype != torch.int32:
+        raise ValueError("topk_ids must be int32")
+    return MoeAlignment(*torch.ops.sglite_awq.awq_moe_align_block_size(topk_ids, block_size, num_experts))
 
 
 _ACT_CODE = {None: _lib.AWQ_MOE_ACT_NONE, "silu": _lib.AWQ_MOE_ACT_SILU, "gelu": _lib.AWQ_MOE_ACT_GELU}
+_ACT_NAME = {"none": None, "silu": "silu", "gelu": "gelu"}
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_moe_w4a16_gemm", mutates_args=("out",), device_types="cuda")
+def _moe_gemm_op(a: torch.Tensor, w: torch.Tensor, s: torch.Tensor, z: torch.Tensor, sorted_ids: torch.Tensor,
+                 expert_offsets: torch.Tensor, topk_weights: Optional[torch.Tensor], out: torch.Tensor, K: int, N: int,
+                 G: int, num_routed: int, top_k: int, activation: str, mul_routed_weight: bool) -> None:
+    E = w.shape[0]
+    with _on_device(a.device):
+        _lib.check(_lib.load().awq_moe_w4a16_gemm(
+            a.data_ptr(), a.shape[0], w.data_ptr(), s.data_ptr(), z.data_ptr(), E, N, K, G, dtype_code(a.dtype),
+            sorted_ids.data_ptr(), sorted_ids.numel(), expert_offsets.data_ptr(), _ptr(topk_weights), num_routed,
+            top_k, _ACT_CODE[_ACT_NAME[activation]], 1 if mul_routed_weight else 0, out.data_ptr(),
+            _stream(a.device)), "awq_moe_w4a16_gemm")
+
+
+@_moe_gemm_op.register_fake
+def _(a, w, s, z, sorted_ids, expert_offsets, topk_weights, out, K, N, G, num_routed, top_k, activation,
+      mul_routed_weight):
+    return None
 
 
 def moe_gemm(a: torch.Tensor, experts: RepackedExperts, K: int, N: int, group_size: int, align: MoeAlignment,
@@ -338,20 +674,36 @@ def moe_gemm(a: torch.Tensor, experts: RepackedExperts, K: int, N: int, group_si
         raise ValueError(f"activation dtype {a.dtype} does not match the scale dtype {experts.s.dtype}")
     if activation not in _ACT_CODE:
         raise ValueError(f"unsupported activation {activation!r}")
+    if mul_routed_weight and topk_weights is None:
+        raise ValueError("mul_routed_weight needs topk_weights")
     G = resolve_group_size(group_size, K)
-    E = experts.w.shape[0]
     ncols = N // 2 if activation is not None else N
     a = _aligned(a)
     if out is None:
         out = torch.empty((num_routed, ncols), dtype=a.dtype, device=a.device)
+    else:
+        _check_out(out, (num_routed, ncols), a.dtype, a.device)
     if topk_weights is not None:
         topk_weights = _aligned(topk_weights.float().reshape(-1), 4)
-    _lib.check(_lib.load().awq_moe_w4a16_gemm(
-        a.data_ptr(), a.shape[0], experts.w.data_ptr(), experts.s.data_ptr(), experts.z.data_ptr(), E, N, K, G,
-        dtype_code(a.dtype), align.sorted_ids.data_ptr(), align.sorted_ids.numel(), align.expert_offsets.data_ptr(),
-        _ptr(topk_weights), num_routed, top_k, _ACT_CODE[activation], 1 if mul_routed_weight else 0, out.data_ptr(),
-        _stream(a.device)), "awq_moe_w4a16_gemm")
+        if topk_weights.numel() < num_routed:
+            raise ValueError(f"topk_weights must hold {num_routed} routed weights, got {topk_weights.numel()}")
+    torch.ops.sglite_awq.awq_moe_w4a16_gemm(a, experts.w, experts.s, experts.z, align.sorted_ids, align.expert_offsets,
+                                            topk_weights, out, K, N, G, num_routed, top_k,
+                                            "none" if activation is None else activation, bool(mul_routed_weight))
     return out
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_moe_sum_reduce", mutates_args=("out",), device_types="cuda")
+def _moe_sum_op(inp: torch.Tensor, out: torch.Tensor) -> None:
+    T, k, H = inp.shape
+    with _on_device(inp.device):
+        _lib.check(_lib.load().awq_moe_sum_reduce(inp.data_ptr(), out.data_ptr(), T, k, H, dtype_code(inp.dtype),
+                                                  _stream(inp.device)), "awq_moe_sum_reduce")
+
+
+@_moe_sum_op.register_fake
+def _(inp, out):
+    return None
 
 
 def moe_sum_reduce(inp: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
@@ -363,7 +715,12 @@ def moe_sum_reduce(inp: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
         raise ValueError("in and out must share a dtype")
     if not (inp.is_contiguous() and out.is_contiguous()):
         raise ValueError("in and out must be contiguous")
-    T, k, H = inp.shape
-    _lib.check(_lib.load().awq_moe_sum_reduce(inp.data_ptr(), out.data_ptr(), T, k, H, dtype_code(inp.dtype),
-                                              _stream(inp.device)), "awq_moe_sum_reduce")
+    torch.ops.sglite_awq.awq_moe_sum_reduce(inp, out)
     return out
+
+
+REGISTERED_OPS: List[str] = [
+    "awq_repack_cdna4", "awq_unrepack_cdna4", "awq_dequant", "awq_dequant_repacked", "awq_w4a16_gemm",
+    "awq_w4a16_gemm_out", "awq_w4a16_gemm_act", "awq_w4a16_gemm_act_out", "awq_repack_experts",
+    "awq_moe_topk_softmax", "awq_moe_align_block_size", "awq_moe_w4a16_gemm", "awq_moe_sum_reduce",
+]

@@ -25,3 +25,17 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def plan():
+    """Planner overrides for one test (awq_set_plan_override), cleared before and after it."""
+    from sglite_amd import ops
+
+    class _Plan:
+        def set(self, knob, value):
+            ops.set_plan_override(knob, int(value))
+
+    ops.clear_plan_overrides()
+    yield _Plan()
+    ops.clear_plan_overrides()

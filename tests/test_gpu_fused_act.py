@@ -31,7 +31,7 @@ def _reference(x, t, G, bias, act):
     return oracle._ACT[act](y).to(x.dtype)
 
 
-def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env=None, monkeypatch=None,
+def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env=None, plan=None,
            kernel=None, seed=0):
     ops = _ops()
     N = 2 * I
@@ -39,7 +39,7 @@ def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env
     r = ops.repack(t["qweight"].to(DEV), t["qzeros"].to(DEV), t["scales"].to(DEV))
     bias = torch.randn(N, generator=torch.Generator().manual_seed(seed + 7)).to(dtype) if with_bias else None
     for k, v in (env or {}).items():
-        monkeypatch.setenv(k, str(v))
+        plan.set(k, v)
     if kernel is not None:
         assert ops.gemm_kernel(M, N, K, G, activation=act) == kernel
     cnt = ops.make_counters(N, DEV)
@@ -64,41 +64,56 @@ def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env
     (300, 1024, 528, "tiled_kernel"),
 ])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_fused_silu_matches_oracle(M, K, I, kernel, dtype, monkeypatch):
-    _check(M, K, I, dtype=dtype, kernel=kernel, monkeypatch=monkeypatch)
+def test_fused_silu_matches_oracle(M, K, I, kernel, dtype, plan):
+    _check(M, K, I, dtype=dtype, kernel=kernel, plan=plan)
+
+
+@pytest.mark.parametrize("M", [7, 8])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_qwen3_4b_gate_up_three_pair_plan(M, dtype, with_bias):
+    """The plan that ships for the Qwen3-4B gate_up at 7-8 rows: three gate/up
+    pairs per workgroup (shape 23054), K = 2560 unsplit, 608 pairs so the last
+    workgroup holds two of three."""
+    ops = _ops()
+    assert ops.plan_info(M, 2 * 9728, 2560, 128, activation="silu").variant == 23054
+    assert ops.workspace_bytes_act(M, 2 * 9728, 2560, 128) == 0
+    _check(M, 2560, 9728, dtype=dtype, with_bias=with_bias, kernel="gemv_kernel")
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu"])
 @pytest.mark.parametrize("M", [1, 12, 64])
-def test_fused_activation_with_bias(act, M, monkeypatch):
-    _check(M, 1024, 272, act=act, with_bias=True, monkeypatch=monkeypatch)
+def test_fused_activation_with_bias(act, M, plan):
+    _check(M, 1024, 272, act=act, with_bias=True, plan=plan)
 
 
 @pytest.mark.parametrize("variant", [21044, 21083, 21084, 22028, 22044, 23054, 24024, 24042])
 @pytest.mark.parametrize("M", [1, 8])
-def test_every_two_tile_gemv_shape(variant, M, monkeypatch):
-    _check(M, 4096, 1040, env={"SGL_AWQ_GEMV_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 8}, kernel="gemv_kernel",
-           monkeypatch=monkeypatch)
+@pytest.mark.parametrize("K", [4096, 2560])
+def test_every_two_tile_gemv_shape(variant, M, K, plan):
+    """Every two-tile GEMV shape, on a K that splits (4096) and one that most shapes take unsplit (2560)."""
+    _check(M, K, 1040, env={"gemv_variant": variant, "gemv_max_m": 8}, kernel="gemv_kernel",
+           plan=plan)
 
 
 @pytest.mark.parametrize("variant", [20202, 20401, 20204])
 @pytest.mark.parametrize("M", [3, 20])
 @pytest.mark.parametrize("G", [32, 64, 128])
-def test_every_two_tile_decode_shape(variant, M, G, monkeypatch):
-    _check(M, 4096, 1040, G=G, env={"SGL_AWQ_SKINNY_VARIANT": variant, "SGL_AWQ_GEMV_MAX_M": 0},
-           kernel="skinny_kernel", monkeypatch=monkeypatch)
+def test_every_two_tile_decode_shape(variant, M, G, plan):
+    _check(M, 4096, 1040, G=G, env={"skinny_variant": variant, "gemv_max_m": 0},
+           kernel="skinny_kernel", plan=plan)
 
 
 @pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("ks", [1, 3])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
-def test_every_prefill_row_block(bm, ks, G, monkeypatch):
+def test_every_prefill_row_block(bm, ks, G, plan):
     K = 1312 if G == 32 else (1280 if G != -1 else 1152)
-    _check(70, K, 1040, G=G, env={"SGL_AWQ_TILED_BM": bm, "SGL_AWQ_TILED_KS": ks, "SGL_AWQ_TILED_MIN_M": 1},
-           kernel="tiled_kernel", monkeypatch=monkeypatch)
+    _check(70, K, 1040, G=G, env={"tiled_bm": bm, "tiled_ks": ks, "tiled_min_m": 1},
+           kernel="tiled_kernel", plan=plan)
 
 
-def test_fused_equals_unfused_gemm_then_activation(monkeypatch):
+def test_fused_equals_unfused_gemm_then_activation(plan):
     """Same kernel and plan with and without the activation: the fused output
     is the plain GEMM's rounded output run through silu in fp32 (prefill
     kernel, no split K), to within one fp16 ulp of the product (the device's
@@ -108,7 +123,7 @@ def test_fused_equals_unfused_gemm_then_activation(monkeypatch):
     N = 2 * I
     t = oracle.make_awq_linear(K, N, G, seed=11)
     r = ops.repack(t["qweight"].to(DEV), t["qzeros"].to(DEV), t["scales"].to(DEV))
-    monkeypatch.setenv("SGL_AWQ_TILED_KS", "1")  # one k-slice: both calls store straight from the accumulators
+    plan.set("tiled_ks", "1")  # one k-slice: both calls store straight from the accumulators
     assert ops.workspace_bytes(M, N, K, G) == 0 and ops.workspace_bytes_act(M, N, K, G) == 0
     x = oracle.make_activation(M, K, seed=12).to(DEV)
     y = ops.gemm(x, r, K, N, G).float()

@@ -170,6 +170,32 @@ def _gpu_reference(x, W):
     return (x.float() @ W.float()).to(x.dtype)
 
 
+def _sample_rows(M):
+    if M <= 64:
+        return torch.arange(M)
+    g = torch.Generator().manual_seed(M)
+    mid = torch.randperm(M - 256, generator=g)[:64] + 128
+    return torch.cat([torch.arange(128), mid.sort().values, torch.arange(M - 128, M)])
+
+
+def _check_full_size(y, W, x, t, K, N, G=128):
+    """A full-size GEMM output against the CPU oracle on sampled rows x three
+    256-column blocks (first, middle, last), the HIP dequantisation of the same
+    blocks bit-exact against the oracle's, and every output against a GPU fp32
+    matmul of that (pinned) dequantised weight."""
+    rows = _sample_rows(x.shape[0])
+    yc = y.cpu()
+    for c0 in sorted({0, (N // 2) // 256 * 256, max(0, N - 256)}):
+        c1 = min(N, c0 + 256)
+        qw, qz, sc = t["qweight"][:, c0 // 8:c1 // 8], t["qzeros"][:, c0 // 8:c1 // 8], t["scales"][:, c0:c1]
+        assert torch.equal(_bits(W[:, c0:c1]), _bits(oracle.dequantize(qw, qz, sc, G))), c0
+        ref = oracle.awq_gemm(x[rows], qw, qz, sc, None, G)
+        ok, err, mx = oracle.tolerance_ok(yc[rows][:, c0:c1], ref, TOL)
+        assert ok, ("oracle block", c0, err, mx)
+    ok, err, mx = oracle.tolerance_ok(y, _gpu_reference(x.to(DEV), W), TOL)
+    assert ok, ("full", err, mx)
+
+
 QWEN3_4B = [(2560, 6144), (4096, 2560), (2560, 19456), (9728, 2560)]
 LLAMA3_8B = [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)]
 
@@ -183,23 +209,24 @@ def test_qwen3_4b_layer_decode(K, N, M):
     W = ops.dequant_repacked(r, K, N, 128)
     W_probe = ops.dequant(d["qweight"], d["qzeros"], d["scales"])
     assert torch.equal(W, W_probe)
-    x = oracle.make_activation(M, K, seed=100 + M).to(DEV)
-    y = ops.gemm(x, r, K, N, 128, counters=ops.make_counters(N, DEV))
-    ok, err, mx = oracle.tolerance_ok(y, _gpu_reference(x, W), TOL)
-    assert ok, (err, mx)
+    x = oracle.make_activation(M, K, seed=100 + M)
+    y = ops.gemm(x.to(DEV), r, K, N, 128, counters=ops.make_counters(N, DEV))
+    _check_full_size(y, W, x, t, K, N)
 
 
 @pytest.mark.parametrize("K,N", LLAMA3_8B)
-@pytest.mark.parametrize("M", [1, 16, 256, 2048])
+@pytest.mark.parametrize("M", [1, 16, 256, 2048, 8192])
 def test_llama3_8b_shapes(K, N, M):
+    """Config 2 at every M it names, up to the reference's largest prefill chunk
+    (max_extend_tokens = 8192, scheduler/config.py:20)."""
     ops = _ops()
     t, d = _linear(K, N, 128, seed=K * 2 + N)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     W = ops.dequant_repacked(r, K, N, 128)
-    x = oracle.make_activation(M, K, seed=200 + M).to(DEV)
-    y = ops.gemm(x, r, K, N, 128, counters=ops.make_counters(N, DEV))
-    ok, err, mx = oracle.tolerance_ok(y, _gpu_reference(x, W), TOL)
-    assert ok, (err, mx)
+    x = oracle.make_activation(M, K, seed=200 + M)
+    y = ops.gemm(x.to(DEV), r, K, N, 128, counters=ops.make_counters(N, DEV))
+    assert y.shape == (M, N)
+    _check_full_size(y, W, x, t, K, N)
 
 
 def test_config0_qkv_against_cpu_oracle():
@@ -290,7 +317,7 @@ def test_hip_graph_capture_replays(M, K, N):
 
 @pytest.mark.parametrize("variant", [10104, 10108, 10116, 10202, 10401, 10404, 20202, 20401, 20204])
 @pytest.mark.parametrize("G", [128, 64, 32])
-def test_every_decode_variant(variant, G, monkeypatch):
+def test_every_decode_variant(variant, G, plan):
     """Each decode-kernel instantiation, with and without cross-workgroup
     split-K, on a K that gives every wave full batches plus a masked tail."""
     ops = _ops()
@@ -300,10 +327,10 @@ def test_every_decode_variant(variant, G, monkeypatch):
     t, d = _linear(K, N, G, seed=variant * 7 + G)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
-    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "0")  # M = 1 too through this kernel
+    plan.set("gemv_max_m", "0")  # M = 1 too through this kernel
     for ks in (1, 3):
-        monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
-        monkeypatch.setenv("SGL_AWQ_SKINNY_KS", str(ks))
+        plan.set("skinny_variant", str(variant))
+        plan.set("skinny_ks", str(ks))
         for M in (1, 9, 17, 32):
             x = oracle.make_activation(M, K, seed=M + ks)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
@@ -314,7 +341,7 @@ def test_every_decode_variant(variant, G, monkeypatch):
 
 
 @pytest.mark.parametrize("M", [1, 20])
-def test_decode_bf16_variants(M, monkeypatch):
+def test_decode_bf16_variants(M, plan):
     ops = _ops()
     K, N, G = 2304, 136, 64
     t, d = _linear(K, N, G, seed=77 + M, dtype=torch.bfloat16)
@@ -322,9 +349,9 @@ def test_decode_bf16_variants(M, monkeypatch):
     cnt = ops.make_counters(N, DEV)
     x = oracle.make_activation(M, K, seed=78, dtype=torch.bfloat16)
     ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
-    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "0")
+    plan.set("gemv_max_m", "0")
     for variant in (10116, 20202, 10401):
-        monkeypatch.setenv("SGL_AWQ_SKINNY_VARIANT", str(variant))
+        plan.set("skinny_variant", str(variant))
         y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
         ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
         assert ok, (variant, err, mx)
@@ -333,7 +360,7 @@ def test_decode_bf16_variants(M, monkeypatch):
 @pytest.mark.parametrize("variant", [11048, 11083, 11084, 11086, 11088, 11165, 11166, 11168, 12083, 12084, 15037,
                                      21044, 21083, 21084, 22028, 22044, 23054, 24024, 24042, 14044])
 @pytest.mark.parametrize("G", [128, -1])
-def test_every_gemv_variant(variant, G, monkeypatch):
+def test_every_gemv_variant(variant, G, plan):
     """Each small-batch GEMV instantiation, with and without cross-workgroup
     split-K, for batch sizes over both m-tile counts (1..32 rows; 1 and 3 rows
     take the biased-operand arithmetic), on a K with a partial last 128-row
@@ -343,10 +370,10 @@ def test_every_gemv_variant(variant, G, monkeypatch):
     t, d = _linear(K, N, G, seed=variant % 997 + (G if G > 0 else 7))
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
-    monkeypatch.setenv("SGL_AWQ_GEMV_MAX_M", "32")
-    monkeypatch.setenv("SGL_AWQ_GEMV_VARIANT", str(variant))
+    plan.set("gemv_max_m", "32")
+    plan.set("gemv_variant", str(variant))
     for ks in (1, 3):
-        monkeypatch.setenv("SGL_AWQ_GEMV_KS", str(ks))
+        plan.set("gemv_ks", str(ks))
         for M in (1, 3, 4, 16, 17, 32):
             x = oracle.make_activation(M, K, seed=M + ks)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
@@ -394,7 +421,7 @@ def test_gemv_bf16_and_bias(M):
 @pytest.mark.parametrize("bm", [32, 64, 128])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_every_tiled_variant(bm, G, dtype, monkeypatch):
+def test_every_tiled_variant(bm, G, dtype, plan):
     """Each prefill-kernel instantiation (row block x groups per 128-row
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
@@ -406,10 +433,10 @@ def test_every_tiled_variant(bm, G, dtype, monkeypatch):
     t, d = _linear(K, N, G, seed=bm + (G if G > 0 else 5), dtype=dtype)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
     cnt = ops.make_counters(N, DEV)
-    monkeypatch.setenv("SGL_AWQ_TILED_BM", str(bm))
-    monkeypatch.setenv("SGL_AWQ_TILED_MIN_M", "1")  # small batches through this kernel too
+    plan.set("tiled_bm", str(bm))
+    plan.set("tiled_min_m", "1")  # small batches through this kernel too
     for ks in (1, 3):  # whole K per workgroup, and three k-slices
-        monkeypatch.setenv("SGL_AWQ_TILED_KS", str(ks))
+        plan.set("tiled_ks", str(ks))
         for M in (20, 33, 130, 257):
             x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
             y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)

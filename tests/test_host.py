@@ -135,7 +135,7 @@ def test_fused_activation_routing():
 def test_invalid_shapes_raise_value_error(K, N, G, dtype, msg):
     lib = _lib.load()
     fake = 0x10000  # never dereferenced: validation fails first
-    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 4, N, K, G, dtype, None, 0, None, None)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 4, N, K, G, dtype, None, 0, None, 0, None)
     assert st == _lib.AWQ_STATUS_INVALID_ARGUMENT
     with pytest.raises(ValueError, match=msg):
         _lib.check(st, "awq_w4a16_gemm")
@@ -144,9 +144,9 @@ def test_invalid_shapes_raise_value_error(K, N, G, dtype, msg):
 def test_null_and_misaligned_pointers_rejected():
     lib = _lib.load()
     fake = 0x10000
-    assert lib.awq_w4a16_gemm(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, None) == -1
+    assert lib.awq_w4a16_gemm(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, 0, None) == -1
     assert "null" in _lib.last_error()
-    assert lib.awq_w4a16_gemm(fake + 2, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, None) == -1
+    assert lib.awq_w4a16_gemm(fake + 2, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None, 0, None, 0, None) == -1
     assert "aligned" in _lib.last_error()
     assert lib.awq_repack_cdna4(fake, fake, fake, 0, 256, 64, 128, fake + 4, fake, fake, None) == -1
     assert lib.awq_dequant(None, fake, fake, 0, 256, 64, 128, fake, None) == -1
@@ -158,42 +158,88 @@ def test_missing_workspace_is_reported_before_launch():
     K, N, M = 28672, 512, 1  # 32 column tiles, 224 k-tiles: the plan splits K across workgroups
     need = lib.awq_workspace_bytes(M, N, K, 128)
     assert need > 0
-    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, None, 0, None, None)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, None, 0, None, 0, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.check(st, "awq_w4a16_gemm")
-    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, None, None)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, None, 0, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE and "counters" in _lib.last_error()
+
+
+def test_short_counters_are_reported_before_launch():
+    lib = _lib.load()
+    fake = 0x10000
+    K, N, M = 28672, 512, 1  # split K on the GEMV kernel: arrival counters needed
+    need = lib.awq_workspace_bytes(M, N, K, 128)
+    cb = lib.awq_counter_bytes(N)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake, cb - 4, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE and "counters of" in _lib.last_error()
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake + 2, cb, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE and "aligned" in _lib.last_error()
+
+
+def test_plan_overrides_and_plan_info():
+    lib = _lib.load()
+    assert lib.awq_set_plan_override(99, 1) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert "knob" in _lib.last_error()
+    assert ops.gemm_kernel(1, 6144, 2560, 128) == "gemv_kernel"
+    with ops.plan_overrides(gemv_max_m=0):
+        assert ops.gemm_kernel(1, 6144, 2560, 128) == "skinny_kernel"
+        with pytest.raises(KeyError):
+            ops.set_plan_override("no_such_knob", 1)
+    assert ops.gemm_kernel(1, 6144, 2560, 128) == "gemv_kernel"
+    with ops.plan_overrides(tiled_min_m=1, tiled_bm=64, tiled_ks=2):
+        info = ops.plan_info(8, 6144, 2560, 128)
+        assert info.kernel == "tiled_kernel" and info.variant == 64 and info.k_slices == 2
+        assert info.workspace_bytes == 2 * 8 * 6144 * 4 and info.threads == 256
+        assert info.workgroups == (6144 // 256) * 1 * 2
+    for M, N, K in [(1, 6144, 2560), (8, 2560, 4096), (32, 19456, 2560), (2048, 28672, 4096)]:
+        info = ops.plan_info(M, N, K, 128)
+        assert info.kernel == ops.gemm_kernel(M, N, K, 128)
+        assert info.workspace_bytes == ops.workspace_bytes(M, N, K, 128)
+        assert info.workgroups >= 1 and info.threads % 64 == 0 and 64 <= info.threads <= 1024
+    assert ops.device_cu_count() >= 1
+
+
+def test_stream_probe_validates_before_launch():
+    lib = _lib.load()
+    fake = 0x10000
+    assert lib.awq_stream_probe(fake, 100, 4, 256, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_stream_probe(fake, 4096, 4, 96, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_stream_probe(fake, 4096, 0, 256, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert lib.awq_stream_probe(fake, 4096, 8, 256, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
+    assert "sink" in _lib.last_error()
+    assert lib.awq_stream_probe(None, 4096, 4, 256, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
 
 
 def test_fused_activation_entry_validates_before_launch():
     lib = _lib.load()
     fake = 0x10000  # never dereferenced: validation fails first
     args = (fake, fake, fake, fake, None, fake)
-    assert lib.awq_w4a16_gemm_act(*args, 4, 64, 256, 128, 0, 3, None, 0, None, None) == -1
+    assert lib.awq_w4a16_gemm_act(*args, 4, 64, 256, 128, 0, 3, None, 0, None, 0, None) == -1
     assert "activation" in _lib.last_error()
-    assert lib.awq_w4a16_gemm_act(*args, 4, 48, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None) == -1
+    assert lib.awq_w4a16_gemm_act(*args, 4, 48, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, 0, None) == -1
     assert "multiple of 32" in _lib.last_error()
     assert lib.awq_w4a16_gemm_act(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, _lib.AWQ_ACT_GELU, None, 0,
-                                  None, None) == -1
+                                  None, 0, None) == -1
     assert "null" in _lib.last_error()
-    assert lib.awq_w4a16_gemm_act(*args, 0, 64, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None) == 0
+    assert lib.awq_w4a16_gemm_act(*args, 0, 64, 256, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, 0, None) == 0
     assert lib.awq_workspace_bytes_act(4, 48, 256, 128) == -1
     # a gate/up projection narrow enough to split K needs the workspace and the counters
     M, N, K = 1, 512, 8192
     need = lib.awq_workspace_bytes_act(M, N, K, 128)
     assert need > 0
-    st = lib.awq_w4a16_gemm_act(*args, M, N, K, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, None)
+    st = lib.awq_w4a16_gemm_act(*args, M, N, K, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, 0, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE
 
 
 def test_m_zero_is_a_noop():
     # an empty batch launches nothing, so no buffer is needed (shape checks still apply)
     lib = _lib.load()
-    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 64, 256, 128, 0, None, 0, None, None) == 0
-    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 60, 256, 128, 0, None, 0, None, None) == -1
+    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 64, 256, 128, 0, None, 0, None, 0, None) == 0
+    assert lib.awq_w4a16_gemm(None, None, None, None, None, None, 0, 60, 256, 128, 0, None, 0, None, 0, None) == -1
     fake = 0x10000
-    assert lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 0, 64, 256, 128, 0, None, 0, None, None) == 0
+    assert lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, 0, 64, 256, 128, 0, None, 0, None, 0, None) == 0
 
 
 # --------------------------------------------------------------------------

@@ -130,6 +130,28 @@ def test_dequant_bf16_exhaustive_pairs_against_bit_rounding():
     np.testing.assert_array_equal(W.view(torch.int16).numpy().view(np.uint16), expect)
 
 
+@pytest.mark.parametrize("K,N,G", [(256, 64, 128), (96, 24, 32), (384, 40, 384), (2560, 1024, 64)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_torch_dequant_is_bit_exact_with_the_numpy_oracle(K, N, G, dtype):
+    """dequantize_torch (the CPU baseline's multithreaded dequantisation) equals dequantize bit for bit."""
+    t = oracle.make_awq_linear(K, N, G, seed=K + N, dtype=dtype)
+    a = oracle.dequantize(t["qweight"], t["qzeros"], t["scales"], G)
+    b = oracle.dequantize_torch(t["qweight"], t["qzeros"], t["scales"], G)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_adversarial_activations_are_finite_and_shaped():
+    for kind in oracle.ADVERSARIAL_KINDS:
+        x = oracle.make_adversarial_activation(3, 2560, kind, seed=1)
+        assert x.shape == (3, 2560) and bool(torch.isfinite(x).all())
+    assert float(oracle.make_adversarial_activation(2, 512, "mean10", 0).float().mean()) > 9.0
+    assert float(oracle.make_adversarial_activation(2, 512, "near_max", 0).float().abs().max()) > 4.0e4
+    ok, ratio = oracle.elementwise_ok(torch.tensor([1.0, 2.0]), torch.tensor([1.0, 2.01]), 1e-2, 0.0)
+    assert ok and ratio < 1.0
+    ok, _ = oracle.elementwise_ok(torch.tensor([1.0, 2.2]), torch.tensor([1.0, 2.0]), 1e-2, 1e-3)
+    assert not ok
+
+
 def test_dequant_rounds_once_not_twice():
     # (q - z) * s with s = 1 + 2^-10 and q - z = 13 - 10: the exact product
     # 3.0029296875 is a tie between two fp16 values and rounds to even
