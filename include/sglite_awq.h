@@ -115,6 +115,24 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype,
                    void* ws, int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream);
 
+/* ---- W4A16 GEMM that allocates nothing --------------------------------------
+ * Same plan, kernels and result as awq_w4a16_gemm (bit-identical output), but
+ * the split-K workspace and arrival counters live in a static device array of
+ * the library (AWQ_NOALLOC_WORKSPACE_BYTES of workspace plus counters for N up
+ * to AWQ_NOALLOC_MAX_N columns, held on every device the library runs on
+ * until the process ends).  For callers that cannot allocate device memory:
+ * code being captured into a HIP graph, tight serving loops, harnesses that
+ * forbid hipMalloc.  The caller passes inputs and outputs only; the call
+ * makes no hipMalloc/hipFree and no allocating library call.  Shapes whose
+ * workspace exceeds the scratch return AWQ_STATUS_UNSUPPORTED.  All calls on
+ * one device share its scratch: calls that overlap in time on one device
+ * (concurrent streams or threads) race and must be serialised by the caller.
+ * No counterpart in the reference. */
+#define AWQ_NOALLOC_WORKSPACE_BYTES (64ll << 20)
+#define AWQ_NOALLOC_MAX_N (1ll << 20)
+int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
+                           int64_t M, int64_t N, int64_t K, int64_t G, int dtype, awq_stream_t stream);
+
 /* ---- W4A16 GEMM with the gated activation fused ----------------------------
  * out[M, N/2] = act(gate) * up, where [gate | up] = x[M, K] @ W (+ bias[N]) are
  * the two column halves of a merged gate_up projection (gate columns first,

@@ -43,6 +43,7 @@ SIGNATURES = {
     "awq_gemm_kernel_kind": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
                               _vp]),
+    "awq_w4a16_gemm_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "awq_workspace_bytes_act": (_i64, [_i64, _i64, _i64, _i64]),
     "awq_gemm_kernel_kind_act": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm_act": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp,
@@ -74,6 +75,9 @@ AWQ_PLAN_SKINNY_KS = 4
 AWQ_PLAN_TILED_MIN_M = 5
 AWQ_PLAN_TILED_BM = 6
 AWQ_PLAN_TILED_KS = 7
+
+AWQ_NOALLOC_WORKSPACE_BYTES = 64 << 20
+AWQ_NOALLOC_MAX_N = 1 << 20
 
 AWQ_MOE_ACT_NONE = 0
 AWQ_MOE_ACT_SILU = 1

@@ -10,6 +10,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/sglite_awq.h"
@@ -103,6 +104,58 @@ int gemm_prepare(const void* x, const void* w, const void* s, const void* z, con
   if (bias && !aligned(bias, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: bias must be 8-byte aligned", who);
   *g = make_geom(M, N, K, Gr);
   *p = plan_gemm(*g);
+  return AWQ_STATUS_OK;
+}
+
+// ---- static scratch of awq_w4a16_gemm_noalloc ------------------------------
+// The split-K workspace (kScratchWsBytes) followed by the arrival counters
+// (kScratchCounterBytes), in device memory that exists from the code
+// object's load to the end of the process, one copy per device.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the
+// device address comes from hipGetSymbolAddress, once per device, and only
+// that address is handed to kernels.
+constexpr int64_t kScratchWsBytes = int64_t(64) << 20;
+constexpr int64_t kScratchCounterBytes = int64_t(256) << 10;
+static __device__ __align__(256) unsigned char scratch[kScratchWsBytes + kScratchCounterBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kScratchDevices];
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of the current device's scratch.  The first call on a device
+// resolves it and, unless `stream` is being captured into a graph, clears the
+// counters on `stream` with a fill kernel (they also start zeroed from the
+// code object's zero-filled data; every GEMM leaves them zero again).
+int scratch_base(hipStream_t stream, char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "hipGetDevice failed");
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_w4a16_gemm_noalloc: device %d beyond the %d supported", dev,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(AWQ_STATUS_HIP_ERROR, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess)
+      return fail(AWQ_STATUS_HIP_ERROR, "hipStreamIsCapturing failed");
+    if (cap == hipStreamCaptureStatusNone) {
+      const int64_t n = kScratchCounterBytes / 4;
+      hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                         (uint32_t*)((char*)ptr + kScratchWsBytes), n);
+      const hipError_t le = hipGetLastError();
+      if (le != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "scratch clear launch: %s", hipGetErrorString(le));
+    }
+    g_scratch_ptr[dev] = (char*)ptr;
+  }
+  *out = g_scratch_ptr[dev];
   return AWQ_STATUS_OK;
 }
 
@@ -227,6 +280,33 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
   }
   return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
                     "awq_w4a16_gemm launch");
+}
+
+int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
+                           int64_t M, int64_t N, int64_t K, int64_t G, int dtype, awq_stream_t stream) {
+  Geom g;
+  GemmPlan p;
+  int st = gemm_prepare(x, w, s, z, bias, out, M, N, K, G, dtype, "awq_w4a16_gemm_noalloc", &g, &p);
+  if (st != 0 || M == 0) return st;
+  void* ws = nullptr;
+  int32_t* counters = nullptr;
+  if (p.ws_bytes > 0) {
+    if (p.ws_bytes > kScratchWsBytes)
+      return fail(AWQ_STATUS_UNSUPPORTED,
+                  "awq_w4a16_gemm_noalloc: this shape's split-K workspace (%lld bytes) exceeds the static scratch "
+                  "of %lld bytes; use awq_w4a16_gemm with a caller workspace",
+                  (long long)p.ws_bytes, (long long)kScratchWsBytes);
+    if (p.kind != 1 && (N + 15) / 16 * 4 > kScratchCounterBytes)
+      return fail(AWQ_STATUS_UNSUPPORTED, "awq_w4a16_gemm_noalloc: N = %lld exceeds the static counters' %lld columns",
+                  (long long)N, (long long)(kScratchCounterBytes / 4 * 16));
+    char* base = nullptr;
+    st = scratch_base((hipStream_t)stream, &base);
+    if (st != 0) return st;
+    ws = base;
+    counters = (int32_t*)(base + kScratchWsBytes);
+  }
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
+                    "awq_w4a16_gemm_noalloc launch");
 }
 
 int64_t awq_workspace_bytes_act(int64_t M, int64_t N, int64_t K, int64_t G) {

@@ -471,6 +471,29 @@ def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Op
     return out
 
 
+def gemm_noalloc(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, out: torch.Tensor,
+                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``gemm`` through awq_w4a16_gemm_noalloc: the split-K workspace and counters are the library's
+    static per-device scratch, so the call allocates nothing (x, out and bias must already be
+    contiguous and aligned).  Calls overlapping on one device race on that scratch."""
+    _require_cuda(x, r.w, out, bias)
+    M = x.shape[0]
+    if x.dim() != 2 or x.shape[1] != K:
+        raise ValueError(f"x must be [M, {K}], got {tuple(x.shape)}")
+    if x.dtype != r.s.dtype:
+        raise ValueError(f"activation dtype {x.dtype} does not match the scale dtype {r.s.dtype}")
+    _check_out(out, (M, N), x.dtype, x.device)
+    if not x.is_contiguous() or (bias is not None and (not bias.is_contiguous() or bias.numel() != N
+                                                       or bias.dtype != x.dtype)):
+        raise ValueError("x (and bias: N elements of x's dtype) must be contiguous")
+    with _on_device(x.device):
+        _lib.check(_lib.load().awq_w4a16_gemm_noalloc(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(),
+                                                      _ptr(bias), out.data_ptr(), M, N, K,
+                                                      resolve_group_size(group_size, K), dtype_code(x.dtype),
+                                                      _stream(x.device)), "awq_w4a16_gemm_noalloc")
+    return out
+
+
 def stream_probe(src: torch.Tensor, nbytes: int, grid: int, block: int, sink: torch.Tensor) -> None:
     """Stream ``nbytes`` of ``src`` with ``grid`` workgroups of ``block`` threads (awq_stream_probe)."""
     _require_cuda(src, sink)

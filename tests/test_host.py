@@ -212,6 +212,18 @@ def test_stream_probe_validates_before_launch():
     assert lib.awq_stream_probe(None, 4096, 4, 256, fake, 16, None) == _lib.AWQ_STATUS_INVALID_ARGUMENT
 
 
+def test_noalloc_entry_rejects_before_launch():
+    lib = _lib.load()
+    fake = 0x10000
+    # 9728 x 2560 at M = 4096 splits K into 80 MiB of partials: beyond the static scratch
+    assert lib.awq_workspace_bytes(4096, 2560, 9728, 128) > _lib.AWQ_NOALLOC_WORKSPACE_BYTES
+    st = lib.awq_w4a16_gemm_noalloc(fake, fake, fake, fake, None, fake, 4096, 2560, 9728, 128, 0, None)
+    assert st == _lib.AWQ_STATUS_UNSUPPORTED and "scratch" in _lib.last_error()
+    assert lib.awq_w4a16_gemm_noalloc(None, fake, fake, fake, None, fake, 4, 64, 256, 128, 0, None) == -1
+    assert lib.awq_w4a16_gemm_noalloc(fake, fake, fake, fake, None, fake, 4, 60, 256, 128, 0, None) == -1
+    assert lib.awq_w4a16_gemm_noalloc(None, None, None, None, None, None, 0, 64, 256, 128, 0, None) == 0
+
+
 def test_fused_activation_entry_validates_before_launch():
     lib = _lib.load()
     fake = 0x10000  # never dereferenced: validation fails first
