@@ -203,6 +203,13 @@ int awq_device_cu_count(void);
 int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activation, int64_t* info);
 int awq_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink, int64_t sink_bytes,
                      awq_stream_t stream);
+/* awq_mfma_probe: `grid` workgroups of `block` threads (64..256), each wave
+ * running `iters` rounds of eight independent v_mfma_f32_32x32x16_f16 on
+ * register operands (8 x 32768 flops per round and wave), one float per wave
+ * to sink (sink_bytes >= 4 * grid *
+ * block / 64): the dense fp16 MFMA rate the device sustains as clocked, the
+ * prefill roofline's attainable ceiling. */
+int awq_mfma_probe(int64_t iters, int64_t grid, int block, float* sink, int64_t sink_bytes, awq_stream_t stream);
 
 /* ---- grouped MoE -------------------------------------------------------------
  * The stages of the fused MoE backend

@@ -53,6 +53,7 @@ SIGNATURES = {
     "awq_device_cu_count": (_int, []),
     "awq_gemm_plan_info": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_i64)]),
     "awq_stream_probe": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _vp]),
+    "awq_mfma_probe": (_int, [_i64, _i64, _int, _vp, _i64, _vp]),
     "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                       ctypes.POINTER(_i64)]),
     "awq_moe_topk_softmax": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]),

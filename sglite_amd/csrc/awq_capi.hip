@@ -399,6 +399,20 @@ int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activatio
   return ok();
 }
 
+int awq_mfma_probe(int64_t iters, int64_t grid, int block, float* sink, int64_t sink_bytes, awq_stream_t stream) {
+  if (iters < 1 || iters >= (int64_t(1) << 40))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_mfma_probe: iters must be in [1, 2^40)");
+  if (grid <= 0 || grid >= (int64_t(1) << 24))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_mfma_probe: grid must be in [1, 2^24)");
+  if (block < 64 || block > 256 || block % 64 != 0)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_mfma_probe: block must be 64, 128, 192 or 256");
+  if (!sink || !aligned(sink, 4)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_mfma_probe: sink must be 4-byte aligned");
+  if (sink_bytes < 4 * grid * (block / 64))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_mfma_probe: sink of %lld bytes needed, %lld given",
+                (long long)(4 * grid * (block / 64)), (long long)sink_bytes);
+  return hip_status(launch_mfma_probe(iters, grid, block, sink, (hipStream_t)stream), "awq_mfma_probe launch");
+}
+
 int awq_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink, int64_t sink_bytes,
                      awq_stream_t stream) {
   if (bytes <= 0 || bytes % 16 != 0)

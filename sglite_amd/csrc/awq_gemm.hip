@@ -296,14 +296,20 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 256 workgroups x (k-tiles per slice + 1), a 64-row step costing 0.75
     // and a 32-row step 0.3 of a 128-row one, plus the partial traffic of the
     // split-K reduction.  The 32-row block serves batches of at most 32 rows.
+    // Row-block codes: 32, 64, 128 = tiled_kernel (16x16x32 MFMAs);
+    // 1064, 1128 = mfma32_kernel (32x32x16 MFMAs) at 64 and 128 rows;
+    // 2064, 2128 = the same with registers for two workgroups per CU.
     const int env_bm = knob(kPlanTiledBm, 0);
-    const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128;
+    const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
+                           env_bm == 2064 || env_bm == 2128;
     const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int bm : {32, 64, 128}) {
-      if (g.K > tiled_max_k(bm) || (env_bm_ok && bm != env_bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
+    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128}) {
+      const int bm = code % 1000;
+      if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
+      if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
       const int64_t tiles = ((g.NT + 15) / 16) * ((g.M + bm - 1) / bm);
       const int64_t min_ktc = g.M <= 32 ? 2 : 4;  // k-tiles per slice at least
       for (int ks : {1, 2, 3, 4, 6, 8, 12, 16}) {
@@ -315,7 +321,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
         if (kse > 1) t += (double)kse * (double)g.M * (double)Np * 4.0 / 3.2e6;
         if (best_bm == 0 || t < best) {
           best = t;
-          best_bm = bm;
+          best_bm = code;
           best_ks = ks;
         }
       }
@@ -324,9 +330,17 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     int64_t ks = env_ks > 0 ? env_ks : best_ks;
     ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
     while (ks > 1 && ks * g.M * Np * 4 >= (int64_t(1) << 31)) --ks;
+    // Grids of at least 1.5 waves of 128-row tiles, unsplit, with at most two
+    // groups per k-tile: the 32x32-MFMA kernel with two workgroups per CU
+    // (Llama-3-8B gate_up at M = 2048: 472 -> 432 us; every linear at
+    // M = 8192: 3-8% faster).  On one wave of tiles the second workgroup has
+    // nothing to overlap with and the 16x16 kernel's deeper prefetch wins.
+    if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64 &&
+        ((g.NT + 15) / 16) * ((g.M + 127) / 128) * 2 >= 3 * (int64_t)g.cus)
+      best_bm = 2128;
     p.variant = best_bm;
     p.grid_x = (g.NT + 15) / 16;
-    p.grid_y = (g.M + best_bm - 1) / best_bm;
+    p.grid_y = (g.M + best_bm % 1000 - 1) / (best_bm % 1000);
     p.ktc = (int)((g.KT + ks - 1) / ks);
     p.ks = (int)((g.KT + p.ktc - 1) / p.ktc);  // every slice gets >= 1 k-tile
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;

@@ -104,6 +104,7 @@ hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s);
 // Streaming probe (awq_probe.hip).
 hipError_t launch_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink,
                                hipStream_t s);
+hipError_t launch_mfma_probe(int64_t iters, int64_t grid, int block, float* sink, hipStream_t s);
 // Threads per workgroup of a plan's main kernel.
 int plan_threads(const GemmPlan& p);
 

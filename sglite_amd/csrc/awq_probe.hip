@@ -10,7 +10,7 @@
 // non-temporal loads before it consumes any, folds them into one word, and
 // each workgroup stores one word (as a GEMM workgroup stores its outputs).
 // The benchmark reports each decode linear against both the HBM peak and this
-// ceiling.  No counterpart in the reference (a measurement kernel).
+// ceiling.  No counterpart in the reference (measurement kernels).
 #include "awq_device.h"
 #include "awq_launch.h"
 
@@ -49,7 +49,45 @@ __global__ __launch_bounds__(1024) void stream_probe_kernel(const u32x4* __restr
   }
 }
 
+// MFMA probe: each wave runs `iters` rounds of eight independent
+// v_mfma_f32_32x32x16_f16 (operands in registers, no memory traffic in the
+// loop) and stores one word; the fp16 MFMA rate a launch of this grid can
+// sustain on the device as clocked, the compute counterpart of the streaming
+// probe.
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16x_acc __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void mfma_probe_kernel(int64_t iters, float* __restrict__ sink) {
+  const int lane = threadIdx.x & 63;
+  h8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(0.001f * (float)((lane + i) & 7));
+    b[i] = (_Float16)(0.002f * (float)((lane * 3 + i) & 7));
+  }
+  f16x_acc acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+  for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+  }
+  float r = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r += acc[j][e];
+  if (lane == 0) sink[blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)] = r;
+}
+
 }  // namespace
+
+hipError_t launch_mfma_probe(int64_t iters, int64_t grid, int block, float* sink, hipStream_t s) {
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3((unsigned)grid), dim3((unsigned)block), 0, s, iters, sink);
+  return hipGetLastError();
+}
 
 hipError_t launch_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink,
                                hipStream_t s) {

@@ -412,6 +412,291 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// 32x32 prefill kernel (v_mfma_f32_32x32x16).
+//
+// Same workgroup tile (BM x 256, 4 waves of 64 columns), pipeline and split-K
+// scheme as tiled_kernel, but every MFMA is a 32x32x16 one: twice the work of
+// a 16x16x32 MFMA per issued instruction, so per k-tile a wave issues half the
+// MFMAs and the same dequantisation and LDS reads, leaving more issue slots for
+// the vector work between them.  A wave owns two groups of 32 columns (tiles
+// 2g, 2g + 1 of its four); per 16-row k-step s the MFMA A operand of lane l is
+// one packed word -- column l % 32 of the group, rows 16 s + 8 (l / 32) .. + 7
+// -- which the tile layout holds in word s / 2 of the 16-byte vector of lane
+// (l % 16) + 16 (l / 32) (even s) or that lane + 32 (odd s) of tile
+// (l % 32) / 16: two 16-byte loads per lane and group per k-tile, from the
+// layout that the other kernels read.  The activation fragments in LDS are
+// [m32 tile][k-step][lane] (lane l: row l % 32, columns 8 (l / 32) .. + 7).
+// Each lane's accumulators hold column m = l % 32 of its m32 tile and the
+// output columns 8 j + 4 (l / 32) .. + 3 (j = 0..3) of its column group.
+// ---------------------------------------------------------------------------
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int GPT>
+struct WStage32 {
+  u32x4 q[2][2];       // [column group][even / odd k-step vector]
+  uint32_t z[2][GPT];  // the zero-point word holding this lane's nibble, per quantisation group
+  uint16_t s[2][GPT];  // this lane's column scale, per quantisation group
+};
+
+template <int BM, int GPT, int NS, int OCC, typename DT>
+__global__ __launch_bounds__(256, OCC) void mfma32_kernel(TiledArgs a) {
+  using E = typename DT::elem;
+  using V8 = typename DT::vec8;
+  using ZS = typename Dq<DT>::ZS;
+  constexpr int MT = BM / 32;              // m32 tiles
+  constexpr int XF = MT * 8;               // activation fragments (1 KiB) per k-tile
+  constexpr int XPW = XF / 4;              // ... loaded by each wave
+  constexpr int kLoadsW = 4 + 4 * GPT;     // weight-stage load instructions per k-tile
+  constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
+  static_assert(kAfterX < 64, "vector-memory counter range");
+  __shared__ u32x4 xs0[XF * 64];
+  __shared__ u32x4 xs1[XF * 64];
+  __shared__ u32x4 xs2[NS > 2 ? XF * 64 : 1];
+  __shared__ u32x4 xs3[NS > 3 ? XF * 64 : 1];
+  auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : xs3)); };
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c32 = lane & 31, h = lane >> 5, c = lane & 15, t = (lane >> 4) & 1;
+  const int tiles = a.gx * a.gy;
+  const int kslice = (int)blockIdx.x / tiles;
+  int bx, by;
+  tile_of((int)blockIdx.x - kslice * tiles, a.gx, a.gy, bx, by);
+  const int kt0 = kslice * a.ktc;
+  const int nsteps = min(a.KT - kt0, a.ktc);
+  const int kend = kt0 + nsteps;
+  const int m0 = by * BM;
+  const int rows = min(BM, a.M - m0);
+  const int K = a.K, KT = a.KT, NG = a.NG;
+  const DqK dk = dq_consts();
+
+  // Activations: fragment f = i * 8 + s (m32 tile i, k-step s) of a k-tile;
+  // wave w loads fragments w * XPW .. w * XPW + XPW - 1.
+  const E* xb = (const E*)a.x + (int64_t)m0 * K;
+  const uint32_t xbytes = (uint32_t)rows * (uint32_t)K * 2u;
+  uint32_t xoff[XPW];
+#pragma unroll
+  for (int j = 0; j < XPW; ++j) {
+    const int f = wave * XPW + j, i = f >> 3, st = f & 7;
+    xoff[j] = (uint32_t)min(i * 32 + c32, rows - 1) * (uint32_t)K * 2u + (uint32_t)(st * 32 + h * 16);
+  }
+
+  // Weights of the wave's two column groups: group g covers slots 2g, 2g + 1
+  // (with a fused gate/up activation: gate tiles t, t + 1 in group 0 and their
+  // up tiles in group 1).  Tiles past the end clamp to the last tile.
+  const int nt0 = bx * 16 + wave * 4;
+  const int NTg = a.NT >> 1;
+  const int pb0 = a.act ? (nt0 >> 1) : nt0;
+  const int pb1 = a.act ? (nt0 >> 1) + NTg : nt0 + 2;
+  int pt[4];
+  bool pv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pt[j] = (j < 2 ? pb0 : pb1) + (j & 1);
+    pv[j] = a.act ? (nt0 >> 1) + (j & 1) < NTg : pt[j] < a.NT;
+  }
+  __amdgpu_buffer_rsrc_t wr[2], zr[2], sr[2];
+  uint32_t woff[2], zoff[2], soff[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int base = min(g == 0 ? pb0 : pb1, a.NT - 1);
+    const uint32_t ntiles = (uint32_t)min(2, a.NT - base);
+    wr[g] = make_rsrc(a.w + (int64_t)base * KT * 64, ntiles * (uint32_t)KT * 1024u);
+    zr[g] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
+    sr[g] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
+    const uint32_t dt = (uint32_t)(min(pt[2 * g + t], a.NT - 1) - base);  // this lane's tile in the range
+    woff[g] = dt * (uint32_t)KT * 1024u + (uint32_t)(c + 16 * h) * 16u;  // + 512 for the odd-step vector
+    zoff[g] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
+    soff[g] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+  }
+  const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.w, 0u);
+  const uint32_t zshift = 4u * (uint32_t)(c & 7);
+
+  f32x16 acc[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][g][e] = 0.f;
+
+  auto load_x = [&](int p, int kt) {
+    u32x4* dst = xbuf(p);
+#pragma unroll
+    for (int j = 0; j < XPW; ++j) {
+      const int f = wave * XPW + j, st = f & 7;
+      const bool kval = kt < kend && kt * 128 + st * 16 < K;  // wave-uniform
+      const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
+      load_lds16(r, &dst[f * 64], xoff[j], kt * 256);
+    }
+  };
+  auto load_w = [&](WStage32<GPT>& S, int kt) {
+    const bool live = kt < kend;
+    kt = min(kt, KT - 1);
+    const int g0 = (kt * 128) >> a.gshift;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const __amdgpu_buffer_rsrc_t rw = live ? wr[g] : r0, rz = live ? zr[g] : r0, rs = live ? sr[g] : r0;
+      S.q[g][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g], kt * 1024, 0);
+      S.q[g][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g] + 512u, kt * 1024, 0);
+#pragma unroll
+      for (int q = 0; q < GPT; ++q) S.z[g][q] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[g] + 8 * q, g0 * 8, 0);
+#pragma unroll
+      for (int q = 0; q < GPT; ++q)
+        S.s[g][q] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[g] + 32 * q, g0 * 32, 0);
+    }
+  };
+  // One k-tile: 8 k-steps of MT x 2 MFMAs.  The LDS reads and the
+  // dequantisation of step s + 1 are issued between step s's MFMAs (one LDS
+  // read and a few vector operations after each MFMA), so no MFMA waits for
+  // an operand produced just before it.
+  auto compute = [&](const WStage32<GPT>& S, const u32x4* xsb) {
+    ZS zs[2][GPT];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int q = 0; q < GPT; ++q) zs[g][q] = Dq<DT>::make((S.z[g][q] >> zshift) & 0xFu, S.s[g][q]);
+    V8 av[2][2];
+    V8 bx[2][MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) bx[0][i] = __builtin_bit_cast(V8, xsb[i * 8 * 64 + lane]);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) av[0][g] = Dq<DT>::word(S.q[g][0][0], zs[g][0], dk);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const int cur = st & 1, nxt = cur ^ 1;
+      if (st + 1 < 8) {
+        const int sn = st + 1;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) bx[nxt][i] = __builtin_bit_cast(V8, xsb[(i * 8 + sn) * 64 + lane]);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) av[nxt][g] = Dq<DT>::word(S.q[g][sn & 1][sn >> 1], zs[g][sn * GPT / 8], dk);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int g = 0; g < 2; ++g) acc[i][g] = mfma32x32x16(av[cur][g], bx[cur][i], acc[i][g]);
+      if (st + 1 < 8) {
+        // 2 MT MFMAs, MT LDS reads and 26 vector operations (two words'
+        // dequantisation) per step: after each MFMA one LDS read (while
+        // there are any) and up to four vector operations.
+#pragma unroll
+        for (int i = 0; i < 2 * MT; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (i < MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  auto sync_step = [&]() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterX));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  WStage32<GPT> stg[NS];
+#pragma unroll
+  for (int p = 0; p + 1 < NS; ++p) {
+    load_x(p, kt0 + p);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(stg[p], kt0 + p);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  sync_step();
+  auto step = [&](int p, int kt) {
+    const int pa = (p + NS - 1) % NS;
+    load_x(pa, kt + NS - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(stg[pa], kt + NS - 1);  // the wait counts rely on this issue order
+    __builtin_amdgcn_sched_barrier(0);
+    compute(stg[p], xbuf(p));
+    sync_step();
+  };
+  int i = 0;
+  for (; i + NS <= nsteps; i += NS) {
+#pragma unroll
+    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p);
+  }
+#pragma unroll
+  for (int p = 0; p + 1 < NS; ++p)
+    if (i + p < nsteps) step(p, kt0 + i + p);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // Output element e of acc[i][g]: row m0 + 32 i + c32, column 8 (e / 4) + 4 h
+  // + e % 4 of group g, i.e. tile slot 2 g + e / 8, column 8 ((e / 4) & 1) +
+  // 4 h + e % 4 of that tile.
+  auto quad = [&](const f32x16& v, int j) { return f32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]}; };
+  const E* bias = (const E*)a.bias;
+  E* out = (E*)a.out;
+  if (a.ks == 1) {
+    if (a.act == kActNone) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int m = i * 32 + c32;
+            const int n0 = pt[2 * g + (j >> 1)] * 16 + 8 * (j & 1) + 4 * h;
+            if (m < rows && n0 < a.N) store4<DT>(out, bias, (int64_t)m0 + m, a.N, n0, quad(acc[i][g], j));
+          }
+    } else {
+      const int Nh = a.N >> 1;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int m = i * 32 + c32;
+          if (m < rows && pv[j >> 1])
+            store4_act<DT>(out, bias, (int64_t)m0 + m, Nh, pt[j >> 1] * 16 + 8 * (j & 1) + 4 * h, Nh,
+                           quad(acc[i][0], j), quad(acc[i][1], j), a.act);
+        }
+    }
+    return;
+  }
+  const int Np = a.NT * 16;
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part + (int64_t)kslice * a.M * Np, (uint32_t)a.M * (uint32_t)Np * 4u);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = i * 32 + c32;
+        const int slot = 2 * g + (j >> 1);
+        const int n0 = pt[slot] * 16 + 8 * (j & 1) + 4 * h;
+        if (m < rows && pv[slot])
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, quad(acc[i][g], j)), pr,
+                                                 ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
+                                                 kCacheDevice);
+      }
+}
+
+// OCC = workgroups per CU the register budget is cut for (2: 256 registers,
+// two waves per SIMD, each workgroup's activation stages in 64 KiB of LDS).
+template <int BM, int NS, int OCC, typename DT>
+hipError_t launch_bm32(const TiledArgs& a, int gpt, hipStream_t s) {
+  const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);
+  switch (gpt) {
+    case 1: hipLaunchKernelGGL((mfma32_kernel<BM, 1, NS, OCC, DT>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((mfma32_kernel<BM, 2, NS, OCC, DT>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((mfma32_kernel<BM, 4, 2, OCC, DT>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int BM, typename DT>
 hipError_t launch_bm(const TiledArgs& a, int gpt, hipStream_t s) {
   const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);
@@ -431,6 +716,10 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
     case 32: return launch_bm<32, DT>(a, gpt, s);
     case 64: return launch_bm<64, DT>(a, gpt, s);
     case 128: return launch_bm<128, DT>(a, gpt, s);
+    case 1064: return launch_bm32<64, 3, 1, DT>(a, gpt, s);
+    case 1128: return launch_bm32<128, 3, 1, DT>(a, gpt, s);
+    case 2064: return launch_bm32<64, 3, 2, DT>(a, gpt, s);
+    case 2128: return launch_bm32<128, 2, 2, DT>(a, gpt, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -505,6 +505,14 @@ def stream_probe(src: torch.Tensor, nbytes: int, grid: int, block: int, sink: to
                    "awq_stream_probe")
 
 
+def mfma_probe(iters: int, grid: int, block: int, sink: torch.Tensor) -> None:
+    """``grid`` x ``block`` threads of back-to-back 32x32x16 fp16 MFMAs (awq_mfma_probe)."""
+    _require_cuda(sink)
+    with _on_device(sink.device):
+        _lib.check(_lib.load().awq_mfma_probe(iters, grid, block, sink.data_ptr(), sink.numel() * sink.element_size(),
+                                              _stream(sink.device)), "awq_mfma_probe")
+
+
 # ---------------------------------------------------------------------------
 # Grouped MoE (experts stacked on dim 0).
 # ---------------------------------------------------------------------------

@@ -418,11 +418,12 @@ def test_gemv_bf16_and_bias(M):
     assert ok, (err, mx)
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128])
+@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_every_tiled_variant(bm, G, dtype, plan):
-    """Each prefill-kernel instantiation (row block x groups per 128-row
+    """Each prefill-kernel instantiation (16x16 MFMA row blocks 32/64/128 and
+    32x32 MFMA row blocks 64/128 (codes 1064/1128) x groups per 128-row
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
     leave the last row block partial; whole pipeline rounds plus a
@@ -445,6 +446,28 @@ def test_every_tiled_variant(bm, G, dtype, plan):
             assert ok, (bm, G, ks, M, err, mx)
     assert int(cnt.abs().sum()) == 0
     assert ops.gemm_kernel(20, N, K, G) == "tiled_kernel"
+
+
+@pytest.mark.parametrize("code", [1064, 1128])
+@pytest.mark.parametrize("K,N", [(4096, 6144), (14336, 4096)])
+def test_mfma32_kernel_at_llama_prefill_sizes(code, K, N, plan):
+    """The 32x32-MFMA prefill kernel at M = 2048 on Llama-3-8B shapes: against the
+    CPU oracle on sampled blocks and the GPU fp32 reference over the pinned
+    dequantised weight, and within fp32-reordering distance of tiled_kernel."""
+    ops = _ops()
+    t, d = _linear(K, N, 128, seed=K + N + code)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    W = ops.dequant_repacked(r, K, N, 128)
+    x = oracle.make_activation(2048, K, seed=code)
+    xd = x.to(DEV)
+    cnt = ops.make_counters(N, DEV)
+    plan.set("tiled_bm", code)
+    y = ops.gemm(xd, r, K, N, 128, counters=cnt)
+    _check_full_size(y, W, x, t, K, N)
+    plan.set("tiled_bm", code % 1000)
+    y_old = ops.gemm(xd, r, K, N, 128, counters=cnt)
+    ok, err, mx = oracle.tolerance_ok(y, y_old, 1e-3)
+    assert ok, (err, mx)
 
 
 @pytest.mark.parametrize("M,K,N,G", [(64, 14336, 4096, 128), (200, 4096, 2560, 64), (40, 2368, 264, 32),
