@@ -44,10 +44,11 @@ Also reported on the same line:
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 
 Profiles (summaries committed under profiles/):
-  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --steps 500 \
+  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --steps 300 \
       --no-cpu-baseline --no-prefill --no-moe --no-stack --no-mlp;  python3 bench.py --rocprof-summary decode <dir>
-  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --no-decode \
-      --no-moe --no-cpu-baseline --no-stack --no-mlp;  python3 bench.py --rocprof-summary prefill <dir>
+  rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --profile-workload NAME;
+      python3 bench.py --rocprof-summary NAME <dir>   (NAME: prefill-2048, prefill-8192, moe, stack70b-64,
+      stack70b-4096, mlp)
   rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) ... -- python3 bench.py --pmc-workload;
       python3 bench.py --pmc-summary <fetch_dir> <write_dir>
 """
@@ -115,7 +116,7 @@ def random_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device
     return ops.Repacked(w, s.view(NT, NG, 16), z.view(NT, NG))
 
 
-def stack70b_bench(ops, dev: torch.device, gen: torch.Generator) -> dict:
+def stack70b_bench(ops, dev: torch.device, gen: torch.Generator, only_m: int = 0) -> dict:
     """Llama-3.1-70B-shaped AWQ stack on one GPU: 80 layers x {qkv 8192->10240,
     o 8192->8192, gate_up 8192->57344, down 28672->8192}, int4 group 128
     (35.6 GB of int4 weights, zeros and scales), run layer after layer at
@@ -129,6 +130,8 @@ def stack70b_bench(ops, dev: torch.device, gen: torch.Generator) -> dict:
     cnts = {name: ops.make_counters(N, dev) for name, K, N in STACK70B}
     res = {}
     for M, passes in ((64, 20), (4096, 3)):
+        if only_m and M != only_m:
+            continue
         xs = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.float16) for _, K, _ in STACK70B}
         outs = {name: torch.empty((M, N), dtype=torch.float16, device=dev) for name, _, N in STACK70B}
 
@@ -513,6 +516,8 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> str:
                 continue
             name = r["Kernel_Name"]
             key = next((k for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel") if k in name), None)
+            if key is None and "mfma32_kernel" in name:  # the 32x32-MFMA member of the tiled kind
+                key = "tiled_kernel"
             if key is None and "copyBuffer" in name:  # torch's device-to-device copy is a runtime blit
                 key = "copy"
             if key is not None:
@@ -570,17 +575,21 @@ def committed_traffic(kernel: str):
 
 
 DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel")
-TRACE_KERNELS = DECODE_KERNELS + ("splitk_reduce_kernel", "moe_")
+# Kernel names of each planner kind in a trace (kind 1 has two kernels).
+KIND_PREFIXES = {"skinny_kernel": ("skinny_kernel<",), "gemv_kernel": ("gemv_kernel<",),
+                 "tiled_kernel": ("tiled_kernel<", "mfma32_kernel<")}
+TRACE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "splitk_reduce_kernel", "moe_",
+                 "topk_softmax_kernel", "align_kernel")
 
 
-def _trace_groups(trace_dir: str):
-    """Kernel-trace durations (us) grouped by (short name, grid, block)."""
+def _trace_rows(trace_dir: str):
+    """(short name, workgroups, grid y, block, start ns, duration us) of the engine's GEMM/MoE dispatches, in
+    time order (probe and torch kernels are left out)."""
     import csv
     import glob
-    from collections import defaultdict
 
-    path = sorted(glob.glob(os.path.join(trace_dir, "*kernel_trace.csv")))[0]
-    groups = defaultdict(list)
+    path = sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True))[0]
+    rows = []
     for r in csv.DictReader(open(path)):
         name = r["Kernel_Name"]
         if not any(k in name for k in TRACE_KERNELS):
@@ -588,8 +597,19 @@ def _trace_groups(trace_dir: str):
         short = name.replace("(anonymous namespace)::", "").replace("sgl_awq::", "").replace("void ", "")
         short = short[:short.index("(")] if "(" in short else short
         bx = int(r["Workgroup_Size_X"])
-        key = (short, int(r["Grid_Size_X"]) // bx, int(r["Grid_Size_Y"]), bx)
-        groups[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        start, end = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        rows.append((short, int(r["Grid_Size_X"]) // bx, int(r["Grid_Size_Y"]), bx, start, (end - start) / 1e3))
+    rows.sort(key=lambda r: r[4])
+    return rows
+
+
+def _trace_groups(trace_dir: str):
+    """Kernel-trace durations (us) grouped by (short name, grid, block)."""
+    from collections import defaultdict
+
+    groups = defaultdict(list)
+    for short, gx, gy, bx, _, d in _trace_rows(trace_dir):
+        groups[(short, gx, gy, bx)].append(d)
     return groups
 
 
@@ -602,34 +622,66 @@ def _trace_table(groups) -> list:
     return lines
 
 
+PROFILE_REPS = 10  # timed calls per shape in the --profile-workload runs (after 2 warm-ups)
+
+
+def _launches_per_call(ops, M: int, N: int, K: int, activation=None) -> int:
+    info = ops.plan_info(M, N, K, G, activation)
+    return 2 if info.kernel == "tiled_kernel" and info.k_slices > 1 else 1
+
+
+def profile_workload(name: str, ops, dev: torch.device, gen: torch.Generator) -> None:
+    """A fixed launch sequence for `rocprofv3 --kernel-trace` (one section of the benchmark, eager calls
+    in a known order), read back by --rocprof-summary NAME."""
+    if name.startswith("prefill"):
+        M = int(name.split("-")[1])
+        x = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
+        for lname, K, N in PREFILL:
+            r = make_repacked(ops, K, N, gen, dev)
+            cnt = ops.make_counters(N, dev)
+            out = torch.empty((M, N), dtype=torch.float16, device=dev)
+            for _ in range(2 + PROFILE_REPS):
+                ops.gemm(x[K], r, K, N, G, counters=cnt, out=out)
+            torch.cuda.synchronize()
+            del r
+    elif name == "moe":
+        moe_bench(ops, dev, gen, reps=20)
+    elif name.startswith("stack70b"):
+        stack70b_bench(ops, dev, gen, only_m=int(name.split("-")[1]))
+    elif name == "mlp":
+        mlp_bench(ops, dev, gen, reps=20)
+    else:
+        raise ValueError(f"unknown profile workload {name!r}")
+    torch.cuda.synchronize()
+    print(f"profile workload {name} done", flush=True)
+
+
 def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
     """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
 
-    decode: every (M, linear) of the step is launched equally often, so a
+    decode: the decode step; every (M, linear) is launched equally often, so a
     kernel's mean algorithmic bytes per launch is the mean over the (M, linear)
-    pairs it serves (ops.gemm_kernel names the kernel of each shape); a split-K
-    GEMM on the tiled kernel also runs splitk_reduce_kernel, listed apart.
-    prefill: the four linears at M = 2048 are each launched 13 times (3
-    warm-up + 10 timed); TFLOP/s = their FLOPs over the summed durations of the
-    tiled (and reduce) kernels.
+    pairs it serves (ops.plan_info names the kernel of each shape); a split-K
+    GEMM on the tiled kernels also runs splitk_reduce_kernel, listed apart.
+    prefill-M (--profile-workload prefill-M): the four Llama-3-8B linears at M,
+    each launched 2 + PROFILE_REPS times in order; per linear the mean of the
+    timed calls (GEMM plus any reduction) and TFLOP/s.
+    moe, stack70b-M, mlp: the section's kernels with their durations.
     """
     from sglite_amd import ops
 
     groups = _trace_groups(trace_dir)
+    head = [f"Command (from the repository root, TMPDIR=/tmp): `{command}`", ""]
     if section == "decode":
-        lines = [
-            "# Decode kernels on the Qwen3-4B layer workload (M = 1, 8, 32), rocprofv3 kernel trace",
-            "",
-            f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
-            "",
+        lines = ["# Decode kernels on the Qwen3-4B layer workload (M = 1, 8, 32), rocprofv3 kernel trace", ""] + head + [
             "Every (M, linear) of the step is launched equally often, so a kernel's mean algorithmic bytes per",
-            "launch is the mean over the (M, linear) pairs it serves.  Split-K GEMMs on the tiled kernel also",
+            "launch is the mean over the (M, linear) pairs it serves.  Split-K GEMMs on the tiled kernels also",
             "launch `splitk_reduce_kernel` (listed in the table, not in the kernel's duration).",
             "",
         ]
         for kern in DECODE_KERNELS:
             pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.gemm_kernel(M, N, K, G) == kern]
-            ds = [d for (k, *_), v in groups.items() if k.startswith(kern + "<") for d in v]
+            ds = [d for (k, *_), v in groups.items() if k.startswith(KIND_PREFIXES[kern]) for d in v]
             if not pairs or not ds:
                 continue
             mean_b = sum(gemm_bytes(*p) for p in pairs) / len(pairs)
@@ -638,24 +690,69 @@ def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
                          f"{len(ds)} dispatches, mean duration {mean_us:.3f} us; mean algorithmic bytes "
                          f"{mean_b / 1e6:.3f} MB; achieved {mean_b / mean_us / 1e3:.1f} GB/s = "
                          f"{mean_b / mean_us / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s.")
+    elif section.startswith("prefill"):
+        M = int(section.split("-")[1])
+        rows = _trace_rows(trace_dir)
+        lines = [f"# Prefill kernels on the Llama-3-8B linears at M = {M}, rocprofv3 kernel trace", ""] + head + [
+            f"Each linear is launched {2 + PROFILE_REPS} times in order (2 warm-ups, {PROFILE_REPS} timed), fp16, "
+            "int4 group 128; a call's duration is its GEMM kernel plus its split-K reduction, if any.",
+            "",
+            "| linear | kernel | calls | mean us per call | TFLOP/s | fraction of 2.5 PFLOP/s |",
+            "|---|---|---|---|---|---|"]
+        i, tot_f, tot_t = 0, 0, 0.0
+        for lname, K, N in PREFILL:
+            per = _launches_per_call(ops, M, N, K)
+            calls = []
+            for c in range(2 + PROFILE_REPS):
+                seg = rows[i:i + per]
+                i += per
+                calls.append((seg[0][0], sum(r[5] for r in seg)))
+            timed = [d for _, d in calls[2:]]
+            us = sum(timed) / len(timed)
+            fl = 2 * M * N * K
+            tot_f += fl * len(timed)
+            tot_t += sum(timed)
+            lines.append(f"| {lname} {K}x{N} | `{calls[-1][0]}` | {len(timed)} | {us:.1f} | {fl / us / 1e6:.1f} | "
+                         f"{fl / us / 1e6 / MFMA_FP16_PEAK_TFLOPS:.4f} |")
+        tf = tot_f / tot_t / 1e6
+        lines += ["", f"* All four linears: {tf:.1f} TFLOP/s = {tf / MFMA_FP16_PEAK_TFLOPS:.4f} of the 2.5 PFLOP/s "
+                  "dense fp16 MFMA peak (FLOPs of the timed calls over their summed kernel durations)."]
+    elif section == "moe":
+        E, H, I, k, T = 128, 2048, 768, 8, 512
+        lines = ["# Grouped MoE kernels, Qwen3-30B-A3B-shaped experts (E=128, H=2048, I=768, top-8, T=512), "
+                 "rocprofv3 kernel trace", ""] + head + [
+            "The forward (top-k softmax, alignment, grouped gate_up GEMM with silu_and_mul, grouped down GEMM",
+            "with the routed weight, top-k sum) replayed as HIP graphs over three expert stacks, then each stage",
+            "on its own; int4 group 128 with zeros, fp16.  Algorithmic bytes of a GEMM: all experts' int4",
+            "weights, zeros and scales plus 2 bytes per element of the routed rows it reads and writes.", ""]
+        stage_b = {"<1, 1,": E * gemm_bytes(0, 2 * I, H) + T * k * (H + I) * 2,
+                   "<1, 0,": E * gemm_bytes(0, H, I) + T * k * (I + H) * 2}
+        tot = 0.0
+        for (n, gx, gy, bx), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            mean = sum(v) / len(v)
+            tot += mean
+            b = next((bb for key, bb in stage_b.items() if n.startswith("moe_gemm_kernel" + key)), None)
+            if b is not None:
+                lines.append(f"* `{n}` (grid {gx} x {gy}): {len(v)} dispatches, mean {mean:.2f} us, "
+                             f"{b / 1e6:.1f} MB -> {b / mean / 1e3:.1f} GB/s = {b / mean / 1e3 / HBM_PEAK_GBS:.4f} "
+                             "of 8 TB/s.")
+        allb = E * (gemm_bytes(0, 2 * I, H) + gemm_bytes(0, H, I)) + T * k * (H + 2 * I + I + H) * 2
+        lines.append(f"* Sum of the stages' mean durations: {tot:.1f} us -> {allb / tot / 1e3:.1f} GB/s = "
+                     f"{allb / tot / 1e3 / HBM_PEAK_GBS:.4f} of 8 TB/s for the forward's {allb / 1e6:.1f} MB.")
+    elif section.startswith("stack70b"):
+        M = int(section.split("-")[1])
+        total = sum(d for v in groups.values() for d in v)
+        n = sum(len(v) for v in groups.values())
+        passes = 22 if M <= 256 else 4  # 2 + 20 graph replays, or 1 + 3 eager passes
+        ms = total / passes / 1e3
+        byt = STACK70B_LAYERS * sum(gemm_bytes(M, N, K) for _, K, N in STACK70B)
+        fl = STACK70B_LAYERS * sum(2 * M * N * K for _, K, N in STACK70B)
+        lines = [f"# Llama-3.1-70B-shaped 80-layer AWQ stack at M = {M}, rocprofv3 kernel trace", ""] + head + [
+            f"* {n} dispatches over {passes} passes (the warm-up included): {ms:.2f} ms of kernel time per pass "
+            f"= {byt / ms / 1e6:.1f} GB/s ({byt / ms / 1e6 / HBM_PEAK_GBS:.4f} of 8 TB/s) and "
+            f"{fl / ms / 1e9:.1f} TFLOP/s ({fl / ms / 1e9 / MFMA_FP16_PEAK_TFLOPS:.4f} of 2.5 PFLOP/s)."]
     else:
-        M = PREFILL_M
-        flops = 13 * sum(2 * M * N * K for _, K, N in PREFILL)
-        us = sum(d for (k, *_), v in groups.items() if k.startswith(("tiled_kernel<", "splitk_reduce_kernel<"))
-                 for d in v)
-        tf = flops / us / 1e6
-        lines = [
-            f"# Prefill kernel on the Llama-3-8B linears at M = {M}, rocprofv3 kernel trace",
-            "",
-            f"Command (from the repository root, TMPDIR=/tmp): `{command}`",
-            "",
-            "Each linear (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, down 14336x4096) is launched 13 times",
-            "(3 warm-up + 10 timed), fp16, int4 group 128.",
-            "",
-            f"* `tiled_kernel`: {sum(len(v) for (k, *_), v in groups.items() if k.startswith('tiled_kernel<'))} "
-            f"dispatches, {us:.1f} us in total for {flops / 1e12:.3f} TFLOP: {tf:.1f} TFLOP/s = "
-            f"{tf / MFMA_FP16_PEAK_TFLOPS:.4f} of 2.5 PFLOP/s dense fp16 MFMA.",
-        ]
+        lines = [f"# {section}, rocprofv3 kernel trace", ""] + head
     lines += [""] + _trace_table(groups)
     return "\n".join(lines) + "\n"
 
@@ -822,11 +919,14 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the decode step (profiling runs of the other sections; no value is reported)")
     ap.add_argument("--rocprof-summary", nargs=2, metavar=("SECTION", "TRACE_DIR"),
-                    help="print a markdown summary (decode or prefill) of a rocprofv3 --kernel-trace run "
+                    help="print a markdown summary (decode or a --profile-workload NAME) of a rocprofv3 --kernel-trace run "
                          "of this script and exit")
     ap.add_argument("--rocprof-command", default="rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- "
                                                   "python3 bench.py <args>",
                     help="the profiled command, quoted in the summary's header")
+    ap.add_argument("--profile-workload", metavar="NAME",
+                    help="run one section's launch sequence for rocprofv3 --kernel-trace and exit: prefill-2048, "
+                         "prefill-8192, moe, stack70b-64, stack70b-4096 or mlp")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -853,6 +953,9 @@ def main() -> int:
     gen = torch.Generator(device=dev).manual_seed(0)
     if args.pmc_workload:
         return pmc_workload(ops, dev, gen)
+    if args.profile_workload:
+        profile_workload(args.profile_workload, ops, dev, gen)
+        return 0
     C = args.copies
     if args.no_decode:
         C = 0

@@ -298,15 +298,16 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // split-K reduction.  The 32-row block serves batches of at most 32 rows.
     // Row-block codes: 32, 64, 128 = tiled_kernel (16x16x32 MFMAs);
     // 1064, 1128 = mfma32_kernel (32x32x16 MFMAs) at 64 and 128 rows;
-    // 2064, 2128 = the same with registers for two workgroups per CU.
+    // 2064, 2128 = the same with registers for two workgroups per CU;
+    // 4032 = the same at 32 rows with registers for four.
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
-                           env_bm == 2064 || env_bm == 2128;
+                           env_bm == 2064 || env_bm == 2128 || env_bm == 4032;
     const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128}) {
+    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032}) {
       const int bm = code % 1000;
       if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
       if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
@@ -328,13 +329,19 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     }
     if (best_bm == 0) best_bm = 64;  // K beyond every limit is rejected by the C ABI
     int64_t ks = env_ks > 0 ? env_ks : best_ks;
-    ks = std::max<int64_t>(1, std::min<int64_t>(ks, g.KT));
+    ks = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(ks, g.KT), 16));  // the reduction takes <= 16
     while (ks > 1 && ks * g.M * Np * 4 >= (int64_t(1) << 31)) --ks;
     // Grids of at least 1.5 waves of 128-row tiles, unsplit, with at most two
     // groups per k-tile: the 32x32-MFMA kernel with two workgroups per CU
     // (Llama-3-8B gate_up at M = 2048: 472 -> 432 us; every linear at
     // M = 8192: 3-8% faster).  On one wave of tiles the second workgroup has
     // nothing to overlap with and the 16x16 kernel's deeper prefetch wins.
+    // Batches of up to 32 rows split in at most 8 k-slices, one group per
+    // k-tile: the 32x32-MFMA kernel at 32 rows with registers for four
+    // workgroups per CU (graph-replay sweep of the Qwen3-4B and Llama-3-8B
+    // linears at M = 16 and 32: 4-12% faster, e.g. Qwen3-4B gate_up at M = 16
+    // 15.1 -> 13.3 us; with 16 slices its longer reduction chains lose).
+    if (!env_bm_ok && best_bm == 32 && ks <= 8 && g.G >= 128) best_bm = 4032;
     if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64 &&
         ((g.NT + 15) / 16) * ((g.M + 127) / 128) * 2 >= 3 * (int64_t)g.cus)
       best_bm = 2128;

@@ -373,10 +373,11 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
 
 // Sum of the k-slices' partials in slice order (deterministic), plus bias, in
 // the output dtype (with a fused gate/up activation: gate and up sums, then
-// act(gate) * up).  One thread per four output columns; the slices are read
-// four at a time, all four loads in flight (slices past ks read as zeros
-// through the buffer range).
-template <typename DT>
+// act(gate) * up).  One thread per four output columns; every slice's 16-byte
+// load is issued before the first is added (KSMAX >= ks loads, the slices past
+// ks read as zeros through the buffer range), so the reduction costs one
+// memory round trip whatever the slice count.
+template <int KSMAX, typename DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
                                                             const typename DT::elem* __restrict__ bias,
                                                             typename DT::elem* __restrict__ out, int M, int N,
@@ -385,16 +386,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const __amdgpu_buffer_rsrc_t r = make_rsrc(part, slice * (uint32_t)ks);
   // Sum of four consecutive partial columns starting at byte offset off.
   auto sum4 = [&](uint32_t off) {
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < ks; k += 4) {
-      f32x4 v[4];
+    f32x4 v[KSMAX];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off + (uint32_t)i * slice,
-                                                                                (int)((uint32_t)k * slice), 0));
+    for (int i = 0; i < KSMAX; ++i)
+      v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, (int)((uint32_t)i * slice), 0));
+    f32x4 sum = v[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sum += v[i];
-    }
+    for (int i = 1; i < KSMAX; ++i) sum += v[i];
     return sum;
   };
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -410,6 +408,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     const f32x4 g = sum4(off), u = sum4(off + (uint32_t)(N / 2) * 4u);
     store4_act<DT>(out, bias, m, No, n0, No, g, u, act);
   }
+}
+
+template <typename DT>
+hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, const Geom& g, int ks, int act,
+                                hipStream_t s) {
+  using E = typename DT::elem;
+  const int64_t quads = g.M * ((act == kActNone ? g.N : g.N / 2) / 4);
+  const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
+  const int M = (int)g.M, N = (int)g.N, Np = (int)(g.NT * 16);
+  if (ks <= 2)
+    hipLaunchKernelGGL((splitk_reduce_kernel<2, DT>), grid, block, 0, s, part, (const E*)bias, (E*)out, M, N, Np, ks, act);
+  else if (ks <= 4)
+    hipLaunchKernelGGL((splitk_reduce_kernel<4, DT>), grid, block, 0, s, part, (const E*)bias, (E*)out, M, N, Np, ks, act);
+  else if (ks <= 8)
+    hipLaunchKernelGGL((splitk_reduce_kernel<8, DT>), grid, block, 0, s, part, (const E*)bias, (E*)out, M, N, Np, ks, act);
+  else if (ks <= 16)
+    hipLaunchKernelGGL((splitk_reduce_kernel<16, DT>), grid, block, 0, s, part, (const E*)bias, (E*)out, M, N, Np, ks,
+                       act);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -720,6 +739,7 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
     case 1128: return launch_bm32<128, 3, 1, DT>(a, gpt, s);
     case 2064: return launch_bm32<64, 3, 2, DT>(a, gpt, s);
     case 2128: return launch_bm32<128, 2, 2, DT>(a, gpt, s);
+    case 4032: return launch_bm32<32, 3, 4, DT>(a, gpt, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -760,15 +780,8 @@ hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const v
   const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
   hipError_t e = dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
   if (e != hipSuccess || p.ks == 1) return e;
-  const int64_t quads = g.M * ((act == kActNone ? g.N : g.N / 2) / 4);
-  const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
-  if (dtype == 0)
-    hipLaunchKernelGGL(splitk_reduce_kernel<F16>, grid, block, 0, s, (const float*)ws, (const _Float16*)bias,
-                       (_Float16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks, act);
-  else
-    hipLaunchKernelGGL(splitk_reduce_kernel<BF16>, grid, block, 0, s, (const float*)ws, (const __bf16*)bias,
-                       (__bf16*)out, (int)g.M, (int)g.N, (int)(g.NT * 16), p.ks, act);
-  return hipGetLastError();
+  return dtype == 0 ? launch_splitk_reduce<F16>((const float*)ws, bias, out, g, p.ks, act, s)
+                    : launch_splitk_reduce<BF16>((const float*)ws, bias, out, g, p.ks, act, s);
 }
 
 }  // namespace sgl_awq
