@@ -107,8 +107,8 @@ int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype,
  * buffer per stream). */
 int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G);
 /* Which kernel awq_w4a16_gemm runs for this shape: 0 = decode split-K kernel,
- * 1 = tiled MFMA kernel, 2 = small-batch GEMV kernel (benchmarks and
- * diagnostics; no counterpart in the reference). */
+ * 1 = tiled MFMA kernel, 2 = small-batch GEMV kernel, 3 = k-slice decode
+ * kernel (benchmarks and diagnostics; no counterpart in the reference). */
 int awq_gemm_kernel_kind(int64_t M, int64_t N, int64_t K, int64_t G);
 int64_t awq_counter_bytes(int64_t N);
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
@@ -167,7 +167,9 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
  *   AWQ_PLAN_SKINNY_KS       decode-kernel k-slices
  *   AWQ_PLAN_TILED_MIN_M     smallest M routed to the tiled kernel
  *   AWQ_PLAN_TILED_BM        tiled row block (32, 64 or 128)
- *   AWQ_PLAN_TILED_KS        tiled k-slices                                   */
+ *   AWQ_PLAN_TILED_KS        tiled k-slices
+ *   AWQ_PLAN_KSLICE_VARIANT  k-slice decode-kernel shape wn*100 + wk*10 + kpw
+ *                            (M <= 32; any other value leaves the plan alone) */
 enum {
   AWQ_PLAN_GEMV_MAX_M = 0,
   AWQ_PLAN_GEMV_VARIANT = 1,
@@ -176,7 +178,8 @@ enum {
   AWQ_PLAN_SKINNY_KS = 4,
   AWQ_PLAN_TILED_MIN_M = 5,
   AWQ_PLAN_TILED_BM = 6,
-  AWQ_PLAN_TILED_KS = 7
+  AWQ_PLAN_TILED_KS = 7,
+  AWQ_PLAN_KSLICE_VARIANT = 8
 };
 int awq_set_plan_override(int knob, int value);
 void awq_clear_plan_overrides(void);

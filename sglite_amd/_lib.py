@@ -76,6 +76,7 @@ AWQ_PLAN_SKINNY_KS = 4
 AWQ_PLAN_TILED_MIN_M = 5
 AWQ_PLAN_TILED_BM = 6
 AWQ_PLAN_TILED_KS = 7
+AWQ_PLAN_KSLICE_VARIANT = 8
 
 AWQ_NOALLOC_WORKSPACE_BYTES = 64 << 20
 AWQ_NOALLOC_MAX_N = 1 << 20

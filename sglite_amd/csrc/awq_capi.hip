@@ -393,7 +393,7 @@ int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activatio
   info[0] = p.kind;
   info[1] = p.variant;
   info[2] = p.ks;
-  info[3] = p.grid_x * p.grid_y * (p.kind == 1 ? p.ks : 1);
+  info[3] = p.grid_x * p.grid_y * (p.kind == 1 || p.kind == 3 ? p.ks : 1);
   info[4] = plan_threads(p);
   info[5] = p.ws_bytes;
   return ok();

@@ -7,7 +7,9 @@
 //  * skinny_kernel (awq_skinny.hip): decode batches up to 32 rows, HBM-bound
 //    split-K;
 //  * tiled_kernel (awq_tiled.hip): prefill (MFMA-bound) and 16-32 rows on
-//    large matrices, split K through a second reduction kernel.
+//    large matrices, split K through a second reduction kernel;
+//  * kslice_kernel (awq_kslice.hip): decode batches up to 32 rows, split K
+//    reduced by the last workgroup of each column group.
 //
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
@@ -32,7 +34,7 @@ namespace {
 // Planner overrides (tests and sweeps only; see awq_set_plan_override).  An
 // unset knob holds kUnset and the planner's own choice stands.
 constexpr int kUnset = INT_MIN;
-std::atomic<int> g_override[kPlanKnobs] = {kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset};
+std::atomic<int> g_override[kPlanKnobs] = {kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset};
 
 int knob(int k, int dflt) {
   const int v = g_override[k].load(std::memory_order_relaxed);
@@ -234,8 +236,51 @@ bool tiled_preferred(const Geom& g, int act) {
   return g.M >= 6 && g.K >= 8192 && g.N >= 8192 && g.N < 32768;
 }
 
+// k-slice kernel plan of shape v (wn * 100 + wk * 10 + kpw): one k-slice of
+// wk * kpw k-tiles per workgroup, column groups of wn * 64 columns (wn * 32
+// gate columns with a fused activation).
+bool plan_kslice(const Geom& g, int v, int act, GemmPlan& p) {
+  if (g.M > 32 || !kslice_variant_ok(v)) return false;
+  const int wn = v / 100, wk = (v / 10) % 10, kpw = v % 10;
+  const int64_t ktc = (int64_t)wk * kpw;
+  const int64_t ks = (g.KT + ktc - 1) / ktc;
+  const int64_t gx = act ? ((g.NT >> 1) + 2 * wn - 1) / (2 * wn) : (g.NT + 4 * wn - 1) / (4 * wn);
+  const int64_t ws = ks > 1 ? ks * g.M * g.NT * 16 * 4 : 0;
+  if (ks > 16 || ws >= (int64_t(1) << 31)) return false;
+  p.kind = 3;
+  p.variant = v;
+  p.ktc = (int)ktc;
+  p.ks = (int)ks;
+  p.grid_x = gx;
+  p.grid_y = 1;
+  p.ws_bytes = ws;
+  return true;
+}
+
+// Where the k-slice kernel (64-column groups, 8 k-tiles per slice, the
+// reduction in the kernel) beats the other decode kernels, from a
+// graph-replay sweep of M = 8, 16, 32 over the Qwen3-4B and Llama-3-8B
+// projections on MI355X: narrow layers (<= 256 column tiles, one group per
+// k-tile) with 17-32 rows and 32-80 k-tiles (o_proj at M = 32: 11.8 ->
+// 10.7 us on Qwen3-4B, 12.1 -> 11.1 us on Llama-3-8B), and from 8 rows when K
+// spans 65-80 k-tiles (Qwen3-4B down: 11.1 -> 10.6, 12.7 -> 11.2 and
+// 14.4 -> 13.5 us at M = 8, 16, 32).  Deeper K (Llama-3-8B down, 112 k-tiles)
+// needs 14 slices and loses to the tiled kernel; wide layers and the fused
+// gate/up activation keep their kernels.
+bool kslice_preferred(const Geom& g, int act) {
+  if (act || g.M < 8 || g.M > 32 || g.NT > 256 || g.G < 128) return false;
+  if (g.KT > 64 && g.KT <= 80) return true;
+  return g.M > 16 && g.KT >= 32 && g.KT <= 80;
+}
+
 GemmPlan plan_gemm(const Geom& g, int act) {
   GemmPlan p{};
+  const int ksv = knob(kPlanKsliceVariant, 0);
+  if (ksv != 0 && plan_kslice(g, ksv, act, p)) return p;
+  // A planner override of any other kernel keeps the k-slice kernel out.
+  const bool forced = knob(kPlanGemvMaxM, -1) >= 0 || knob(kPlanTiledMinM, 0) > 0 ||
+                      knob(kPlanSkinnyVariant, 0) != 0 || knob(kPlanGemvVariant, 0) != 0 || knob(kPlanTiledBm, 0) != 0;
+  if (!forced && ksv == 0 && kslice_preferred(g, act) && plan_kslice(g, 142, act, p)) return p;
   const bool tiled = tiled_preferred(g, act);
   if (!tiled && gemv_preferred(g, act) && plan_gemv(g, p, act)) return p;
   if (!tiled) {
@@ -356,7 +401,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
 }
 
 int plan_threads(const GemmPlan& p) {
-  if (p.kind == 1) return 256;
+  if (p.kind == 1 || p.kind == 3) return 256;
   if (p.kind == 2) return 64 * ((p.variant / 1000) % 10) * ((p.variant / 10) % 100);
   return 64 * ((p.variant / 100) % 100) * (p.variant % 100);
 }
@@ -366,6 +411,7 @@ hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const vo
                        hipStream_t s) {
   if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
   if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
+  if (p.kind == 3) return launch_kslice(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
   return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
 }
 

@@ -28,7 +28,8 @@ enum : int {
   kPlanTiledMinM = 5,     // smallest M routed to the tiled kernel
   kPlanTiledBm = 6,       // tiled row block (32, 64, 128)
   kPlanTiledKs = 7,       // tiled k-slices
-  kPlanKnobs = 8
+  kPlanKsliceVariant = 8, // in-kernel split-K decode kernel shape wn*100 + wk*10 + kpw
+  kPlanKnobs = 9
 };
 bool set_plan_override(int knob, int value);
 void clear_plan_overrides();
@@ -44,7 +45,8 @@ hipError_t launch_dequant_repacked(const void* w, const void* sr, const void* zr
 
 // GEMM plan: which kernel and how K is split.
 struct GemmPlan {
-  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM, 2 = GEMV (M <= 32)
+  int kind;      // 0 = skinny (M <= 32), 1 = tiled MFMA GEMM, 2 = GEMV (M <= 32),
+                 // 3 = k-slice kernel (M <= 32, split-K reduced in the kernel)
   int variant;   // kernel template selector
   int ks;        // k-splits across workgroups
   int ktc;       // k-tiles per workgroup
@@ -64,6 +66,10 @@ bool gemv_variant_ok(int v);
 hipError_t launch_gemv(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                        hipStream_t s);
+bool kslice_variant_ok(int v);
+hipError_t launch_kslice(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
+                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
+                         hipStream_t s);
 int64_t tiled_max_k(int bm);
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,

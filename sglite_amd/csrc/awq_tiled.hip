@@ -39,6 +39,7 @@
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
 // and gptq_marlin_gemm (marlin_utils.py:388-410) for large batches.
+#include "awq_buffer.h"
 #include "awq_device.h"
 #include "awq_epilogue.h"
 #include "awq_launch.h"
@@ -46,24 +47,6 @@
 namespace sgl_awq {
 
 namespace {
-
-constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
-constexpr int kCacheDevice = 16;              // buffer cache policy: device scope (sc1)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);
-}
-
-// One 16-byte buffer load per lane straight into LDS: lane l's bytes land at
-// dst + 16 * l (dst is wave-uniform).
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
-}
-
-// s_waitcnt immediate that waits until at most n vector-memory loads are
-// outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 struct TiledArgs {
   const void* x;
@@ -449,22 +432,6 @@ hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, 
 // Each lane's accumulators hold column m = l % 32 of its m32 tile and the
 // output columns 8 j + 4 (l / 32) .. + 3 (j = 0..3) of its column group.
 // ---------------------------------------------------------------------------
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f32x16 mfma32x32x16(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-template <int GPT>
-struct WStage32 {
-  u32x4 q[2][2];       // [column group][even / odd k-step vector]
-  uint32_t z[2][GPT];  // the zero-point word holding this lane's nibble, per quantisation group
-  uint16_t s[2][GPT];  // this lane's column scale, per quantisation group
-};
 
 template <int BM, int GPT, int NS, int OCC, typename DT>
 __global__ __launch_bounds__(256, OCC) void mfma32_kernel(TiledArgs a) {

@@ -231,7 +231,7 @@ def workspace_bytes_act(M: int, N: int, K: int, group_size: int) -> int:
     return _lib.check(_lib.load().awq_workspace_bytes_act(M, N, K, G), "awq_workspace_bytes_act")
 
 
-KERNEL_NAMES = {0: "skinny_kernel", 1: "tiled_kernel", 2: "gemv_kernel"}
+KERNEL_NAMES = {0: "skinny_kernel", 1: "tiled_kernel", 2: "gemv_kernel", 3: "kslice_kernel"}
 
 
 def gemm_kernel(M: int, N: int, K: int, group_size: int, activation: Optional[str] = None) -> str:
@@ -265,7 +265,8 @@ def plan_info(M: int, N: int, K: int, group_size: int, activation: Optional[str]
 PLAN_KNOBS = {"gemv_max_m": _lib.AWQ_PLAN_GEMV_MAX_M, "gemv_variant": _lib.AWQ_PLAN_GEMV_VARIANT,
               "gemv_ks": _lib.AWQ_PLAN_GEMV_KS, "skinny_variant": _lib.AWQ_PLAN_SKINNY_VARIANT,
               "skinny_ks": _lib.AWQ_PLAN_SKINNY_KS, "tiled_min_m": _lib.AWQ_PLAN_TILED_MIN_M,
-              "tiled_bm": _lib.AWQ_PLAN_TILED_BM, "tiled_ks": _lib.AWQ_PLAN_TILED_KS}
+              "tiled_bm": _lib.AWQ_PLAN_TILED_BM, "tiled_ks": _lib.AWQ_PLAN_TILED_KS,
+              "kslice_variant": _lib.AWQ_PLAN_KSLICE_VARIANT}
 
 
 def set_plan_override(knob: str, value: int) -> None:

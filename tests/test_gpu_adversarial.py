@@ -4,7 +4,8 @@ The fp16 decode paths do not dequantise to rnd((q - z) * s) per weight: the
 GEMV kernel at 1-3 rows and the skinny kernel feed the MFMAs the biased
 nibbles B + q (B = 1024 fp16, 128 bf16) and subtract s * (B + z) * sum(x) in
 fp32; the GEMV kernel at 4-16 rows feeds the exact integers q - z and scales
-the fp32 sums.  Their accuracy rests on fp32 headroom that zero-mean N(0, 1)
+the fp32 sums.  (The tiled and k-slice kernels dequantise bit-exactly into
+their MFMA operands.)  Their accuracy rests on fp32 headroom that zero-mean N(0, 1)
 activations never test, so every path here runs activations with a large
 mean, outlier channels (x300, +-1000) and fp16-extreme channels (+-5e4), in
 fp16 and bf16, and is held to the GEMM contract (max|err| <= 2e-2 * max|ref|)
@@ -90,3 +91,13 @@ def test_fused_gate_up_paths(M, kind):
 def test_tiled_dequant_path(dtype, kind):
     """The prefill kernel (bit-exact dequantisation into the MFMAs) at 48 rows, split K."""
     _run(48, 4096, 1024, dtype, kind, kernel="tiled_kernel")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [8, 32])
+def test_kslice_dequant_path(M, dtype, kind):
+    """The k-slice decode kernel (bit-exact dequantisation into 32x32 MFMAs, the split-K
+    reduction in the kernel) on the Qwen3-4B down and o_proj shapes."""
+    K, N = (9728, 2560) if M == 8 else (4096, 2560)
+    _run(M, K, N, dtype, kind, kernel="kslice_kernel")

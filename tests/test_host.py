@@ -82,7 +82,7 @@ def test_workspace_query_is_bounded():
     (2560, 6144, "g" * 16),                    # Qwen3-4B qkv: short K, GEMV throughout
     (4096, 2560, "g" * 4 + "s" * 12),          # Qwen3-4B o_proj: narrow, 32 k-tiles
     (2560, 19456, "g" * 13 + "t" * 3),         # Qwen3-4B gate_up
-    (9728, 2560, "g" * 16),                    # Qwen3-4B down: split K keeps 26 k-tiles per workgroup
+    (9728, 2560, "g" * 7 + "k" * 9),           # Qwen3-4B down: 76 k-tiles, k-slice kernel from 8 rows
     (4096, 6144, "g" * 16),                    # Llama-3-8B qkv
     (4096, 28672, "g" * 4 + "s" * 9 + "t" * 3),  # Llama-3-8B gate_up: wide
     (14336, 4096, "g" * 9 + "t" * 7),          # Llama-3-8B down: deep
@@ -91,11 +91,30 @@ def test_workspace_query_is_bounded():
     (28672, 8192, "g" * 5 + "t" * 11),         # Llama-3-70B down
 ])
 def test_decode_routing(K, N, routes):
-    """Kernel choice for 1..16 rows (g = GEMV, s = skinny decode kernel, t = tiled)."""
-    names = {"g": "gemv_kernel", "s": "skinny_kernel", "t": "tiled_kernel"}
+    """Kernel choice for 1..16 rows (g = GEMV, s = skinny decode kernel, t = tiled, k = k-slice)."""
+    names = {"g": "gemv_kernel", "s": "skinny_kernel", "t": "tiled_kernel", "k": "kslice_kernel"}
     got = "".join(next(k for k, v in names.items() if v == ops.gemm_kernel(M, N, K, 128))
                   for M in range(1, len(routes) + 1))
     assert got == routes, (K, N)
+
+
+def test_kslice_routing_at_17_to_32_rows():
+    """Narrow layers with 32-80 k-tiles take the k-slice kernel from 17 rows
+    (o_proj), 65-80 k-tiles from 8 rows; deeper K, wide layers and the fused
+    activation keep their kernels."""
+    for M in (17, 24, 32):
+        assert ops.gemm_kernel(M, 2560, 4096, 128) == "kslice_kernel"
+        assert ops.gemm_kernel(M, 4096, 4096, 128) == "kslice_kernel"
+        assert ops.gemm_kernel(M, 2560, 9728, 128) == "kslice_kernel"
+        assert ops.gemm_kernel(M, 4096, 14336, 128) != "kslice_kernel"  # 112 k-tiles
+        assert ops.gemm_kernel(M, 6144, 2560, 128) != "kslice_kernel"   # 384 column tiles
+        assert ops.gemm_kernel(M, 2560, 4096, 64) != "kslice_kernel"    # two groups per k-tile
+    assert ops.gemm_kernel(16, 2560, 4096, 128) != "kslice_kernel"
+    assert ops.gemm_kernel(8, 2560, 9728, 128) == "kslice_kernel"
+    assert ops.gemm_kernel(7, 2560, 9728, 128) != "kslice_kernel"
+    assert ops.gemm_kernel(32, 2 * 1280, 4096, 128, activation="silu") != "kslice_kernel"
+    info = ops.plan_info(32, 2560, 4096, 128)
+    assert info.variant == 142 and info.k_slices == 4 and info.workgroups == 160
 
 
 def test_gemv_keeps_deep_k_unsplit_at_few_rows():
@@ -193,6 +212,19 @@ def test_plan_overrides_and_plan_info():
         assert info.kernel == "tiled_kernel" and info.variant == 64 and info.k_slices == 2
         assert info.workspace_bytes == 2 * 8 * 6144 * 4 and info.threads == 256
         assert info.workgroups == (6144 // 256) * 1 * 2
+    with ops.plan_overrides(kslice_variant=141):
+        # o_proj 4096 x 2560 at M = 32: 64-column groups, 4 k-tiles per slice
+        info = ops.plan_info(32, 2560, 4096, 128)
+        assert info.kernel == "kslice_kernel" and info.variant == 141 and info.k_slices == 8
+        assert info.workgroups == 40 * 8 and info.threads == 256
+        assert info.workspace_bytes == 8 * 32 * 2560 * 4
+        # fused gate/up: 32 gate columns per wave
+        info = ops.plan_info(16, 2 * 1040, 2048, 128, "silu")
+        assert info.kernel == "kslice_kernel" and info.workgroups == 33 * 4  # 65 gate tiles, two per wave
+        assert ops.plan_info(33, 2560, 4096, 128).kernel != "kslice_kernel"  # one 32-row block only
+        assert ops.plan_info(32, 2560, 4096 * 5, 128).kernel != "kslice_kernel"  # > 16 slices
+    with ops.plan_overrides(kslice_variant=999):  # not instantiated: ignored
+        assert ops.plan_info(32, 2560, 4096, 128).kernel != "kslice_kernel"
     for M, N, K in [(1, 6144, 2560), (8, 2560, 4096), (32, 19456, 2560), (2048, 28672, 4096)]:
         info = ops.plan_info(M, N, K, 128)
         assert info.kernel == ops.gemm_kernel(M, N, K, 128)
