@@ -515,7 +515,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> str:
             if r["Counter_Name"] != counter:
                 continue
             name = r["Kernel_Name"]
-            key = next((k for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel") if k in name), None)
+            key = next((k for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel", "kslice_kernel") if k in name), None)
             if key is None and "mfma32_kernel" in name:  # the 32x32-MFMA member of the tiled kind
                 key = "tiled_kernel"
             if key is None and "copyBuffer" in name:  # torch's device-to-device copy is a runtime blit
@@ -549,14 +549,14 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> str:
         "| kernel | dispatches | FETCH_SIZE (MB) | WRITE_SIZE (MB) | calibrated traffic (MB) | algorithmic (MB) |",
         "|---|---|---|---|---|---|",
     ]
-    for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel"):
+    for k in DECODE_KERNELS:
         if k not in fetch or k not in write:
             continue
         t = fetch[k] * cf + write[k] * cw
         a = sum(algo[k]) / len(algo[k]) if algo[k] else float("nan")
         lines.append(f"| `{k}` | {nf[k]} | {fetch[k] / 1e6:.3f} | {write[k] / 1e6:.3f} | {t / 1e6:.3f} | {a / 1e6:.3f} |")
     lines.append("")
-    for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel"):
+    for k in DECODE_KERNELS:
         if k in fetch and k in write:
             lines.append(f"traffic_bytes_per_launch {k} {int(fetch[k] * cf + write[k] * cw)}")
     return "\n".join(lines) + "\n"
@@ -574,12 +574,12 @@ def committed_traffic(kernel: str):
     return None
 
 
-DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel")
+DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "kslice_kernel")
 # Kernel names of each planner kind in a trace (kind 1 has two kernels).
 KIND_PREFIXES = {"skinny_kernel": ("skinny_kernel<",), "gemv_kernel": ("gemv_kernel<",),
-                 "tiled_kernel": ("tiled_kernel<", "mfma32_kernel<")}
+                 "tiled_kernel": ("tiled_kernel<", "mfma32_kernel<"), "kslice_kernel": ("kslice_kernel<",)}
 TRACE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "splitk_reduce_kernel", "moe_",
-                 "topk_softmax_kernel", "align_kernel")
+                 "topk_softmax_kernel", "align_kernel", "kslice_kernel")
 
 
 def _trace_rows(trace_dir: str):
