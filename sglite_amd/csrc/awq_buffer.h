@@ -11,6 +11,8 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (
 // agent-scope atomic load or store, so such an access is coherent across the
 // XCDs' L2 caches once it has completed.
 constexpr int kCacheDevice = 16;
+// Buffer cache policy NT (non-temporal): a stream read once.
+constexpr int kCacheStream = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kRsrcWord3);

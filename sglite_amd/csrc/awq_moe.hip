@@ -15,10 +15,11 @@
 //                             writing [T * k, H]    (second GEMM)
 //   moe_sum_kernel        out[t] = sum_j y[t * k + j] in fp32, cast once
 //
-// The grouped GEMM stages the gathered activation rows through double-buffered
-// LDS in MFMA fragment order (like the prefill kernel) so the four waves of a
-// workgroup share one copy, and each wave dequantises the weights of its own
-// 64 columns straight from global memory into MFMA operands.  A workgroup
+// The grouped GEMM keeps a pass's gathered activation rows resident in LDS in
+// MFMA fragment order (up to 128 KiB) so the eight waves of a workgroup share
+// one copy and then run without meeting each other; each wave dequantises the
+// weights of its own 32 columns straight from global memory into MFMA
+// operands, several k-tiles ahead.  A workgroup
 // serves every block of one expert for its column slice, so each expert's
 // weights are streamed from HBM once per forward; workgroups of one expert are
 // placed on one XCD so the expert's activation rows are fetched into one L2.
@@ -26,6 +27,7 @@
 
 #include <algorithm>
 
+#include "awq_buffer.h"
 #include "awq_device.h"
 #include "awq_launch.h"
 
@@ -302,9 +304,7 @@ struct MoeArgs {
 
 // Workgroup shape: 8 waves (two per SIMD), each owning two 16-column tiles
 // (256 columns per workgroup, or 128 gate + 128 up columns with a gate/up
-// activation), so the gathered activation tile in LDS feeds 16 tiles; with
-// three k-tiles of loads in flight per wave one workgroup fills a CU's
-// registers.
+// activation), so the gathered activation rows in LDS feed 16 tiles.
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTilesPerWave = 2;
@@ -312,12 +312,22 @@ constexpr int kTilesPerWave = 2;
 // takes more passes, spread over grid.y so that they run side by side and
 // share the expert's weights through L2.
 constexpr int kMaxMt = 4;
-constexpr int kXsBuf = kMaxMt * 4 * 64;  // one LDS buffer: [m-tile][k-block][lane]
-constexpr int kXsBufs = 2;
+// The pass's activation rows stay resident in LDS for a chunk of k-tiles:
+// 128 KiB = 128 fragments of 1 KiB ([k-tile][m-tile][k-block][lane]), i.e.
+// up to 32 / MC k-tiles for MC m-tiles, in whole loop iterations (all of
+// K = 2048 at up to two m-tiles, all of K = 768 at four).  Within a chunk the
+// waves never wait for each other.
+constexpr int kXsFrags = 128;
+
+// Weight k-tiles held in registers per wave (NS: the one being multiplied and
+// NS - 1 in flight): the host picks 4, or 3 where K spans a multiple of three
+// k-tiles but not of four (the k loop is padded to a multiple of NS), and 3
+// with four quantisation groups per k-tile (their zero and scale words take
+// the registers).
 
 // One pass over K for MC m-tiles (16 routed rows each) starting at sorted row
 // rb.  The wave's column tiles are ntc[0..1] (expert-local tile indices).
-template <int MC, int GPT, int EPI, typename DT>
+template <int MC, int GPT, int EPI, int NS, typename DT>
 __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ xs, const u32x4* __restrict__ we,
                                          const uint16_t* __restrict__ se, const uint64_t* __restrict__ ze,
                                          const int (&ntc)[kTilesPerWave], const int (&ncol)[kTilesPerWave], int rb,
@@ -327,11 +337,10 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   using V4 = typename DT::vec4;
   using ZS = typename Dq<DT>::ZS;
   constexpr int TW = kTilesPerWave;
-  constexpr int BPG = 4 / GPT;                           // 32-row k-blocks per group
-  constexpr int NFRAG = MC * 4;                          // activation fragments per k-tile
-  constexpr int FPT = (NFRAG + kWaves - 1) / kWaves;     // fragments loaded per thread
+  constexpr int BPG = 4 / GPT;               // 32-row k-blocks per group
+  constexpr int KC = kXsFrags / (MC * 4);    // k-tiles per resident activation chunk
   const int c = lane & 15, lg = lane >> 4;
-  const void* x = a.x;
+  const int KT = a.KT;
   const DqK dk = dq_consts();
 
   // Routed row of lane column c in each m-tile (the loader and the epilogue
@@ -339,23 +348,42 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   // output column m depends on activation row m only).
   int sid[MC];
   bool sval[MC];
+  uint32_t xrow[MC];  // byte offset of the lane's activation row (the host keeps `a` below 4 GiB)
 #pragma unroll
   for (int i = 0; i < MC; ++i) {
     sid[i] = a.sorted[rb + i * 16 + c];
     sval[i] = sid[i] >= 0 && sid[i] < a.num_routed;
+    xrow[i] = (uint32_t)(sval[i] ? sid[i] / a.a_div : 0) * (uint32_t)a.K * 2u + (uint32_t)lg * 16u;
   }
-  // Loader: thread (wave, lane) fetches fragments f = wave + kWaves * i
-  // (m-tile f / 4, k-block f % 4) of each k-tile.
-  uint32_t xrow[FPT];  // byte offset of the fragment's row (the host keeps `a` below 4 GiB)
+
+  // Activation chunk [kc0, kc1) -> LDS: fragment f = (k-tile - kc0, m-tile,
+  // k-block) of 16 rows x 32 k, lane (c, lg) bringing row c's 8 elements at
+  // 8 lg.  Wave w takes fragments w, w + 8, ..., eight loads in flight before
+  // their LDS stores (a fragment index past the end repeats the last one).
+  // k-blocks past K store zeros.
+  auto load_chunk = [&](int kc0, int kc1) {
+    const int nf = (kc1 - kc0) * MC * 4;
+    for (int f0 = wave; f0 < nf; f0 += 8 * kWaves) {
+      u32x4 v[8];
 #pragma unroll
-  for (int i = 0; i < FPT; ++i) {
-    const int mt = min(wave + kWaves * i, NFRAG - 1) >> 2;
-    int r = 0;
+      for (int i = 0; i < 8; ++i) {
+        const int f = min(f0 + i * kWaves, nf - 1);
+        const int w = f & 3, mt = (f >> 2) % MC, kt = kc0 + (f >> 2) / MC;
+        uint32_t row = xrow[0];
 #pragma unroll
-    for (int m = 0; m < MC; ++m)
-      if (m == mt) r = sval[m] ? sid[m] / a.a_div : 0;
-    xrow[i] = (uint32_t)r * (uint32_t)a.K * 2u;
-  }
+        for (int q = 1; q < MC; ++q)
+          if (mt == q) row = xrow[q];
+        const uint32_t k0 = (uint32_t)min(kt * 128 + w * 32, a.K - 32);
+        v[i] = ld_off<u32x4>(a.x, row + k0 * 2u);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int f = min(f0 + i * kWaves, nf - 1);
+        const int w = f & 3, kt = kc0 + (f >> 2) / MC;
+        xs[f * 64 + lane] = kt * 128 + w * 32 < a.K ? v[i] : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
 
   f32x4 acc[MC][TW];
 #pragma unroll
@@ -363,104 +391,113 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
 #pragma unroll
     for (int j = 0; j < TW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Per-tile byte offsets inside the expert.
-  uint32_t woff[TW], goff[TW];
+  // The expert's weights, zero words and scales as buffer resources (explicit
+  // global loads with the k-tile and group offsets in scalar registers);
+  // per-tile byte offsets inside them.
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(we, (uint32_t)(a.w_stride * 16));
+  const __amdgpu_buffer_rsrc_t zr = make_rsrc(ze, (uint32_t)(a.z_stride * 8));
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(se, (uint32_t)(a.s_stride * 2));
+  uint32_t woff[TW], zoff[TW], soff[TW];
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
-    woff[j] = ((uint32_t)ntc[j] * (uint32_t)a.KT * 64u + lane) * 16u;
-    goff[j] = (uint32_t)ntc[j] * (uint32_t)a.NG;
+    woff[j] = ((uint32_t)ntc[j] * (uint32_t)KT * 64u + lane) * 16u;
+    zoff[j] = (uint32_t)ntc[j] * (uint32_t)a.NG * 8u + (uint32_t)(c >> 3) * 4u;
+    soff[j] = ((uint32_t)ntc[j] * (uint32_t)a.NG * 16u + (uint32_t)c) * 2u;
   }
 
-  // Everything one k-tile needs from global memory.  Three stages rotate
-  // (the loop is unrolled by three, so no register copy waits for a load):
-  // weights are loaded two k-tiles ahead of their use, activations two tiles
-  // ahead of their LDS store.
+  // A k-tile's weights, zero points and scales for the wave's two tiles.
   struct Stage {
-    u32x4 q[TW];           // weight words of the wave's column tiles
-    uint32_t z[TW][GPT];   // zero-point word holding the lane's nibble
-    uint16_t s[TW][GPT];   // scale bits (kept 16-bit: a widening would wait for the load at once)
-    u32x4 xr[FPT];         // activation fragments bound for LDS
+    u32x4 q[TW];          // weight words of the wave's column tiles
+    uint32_t z[TW][GPT];  // zero-point word holding the lane's nibble
+    uint16_t s[TW][GPT];  // scale bits (kept 16-bit: a widening would wait for the load at once)
   };
-  auto load = [&](int kt, Stage& st) {
-    // k-blocks past K (K % 128 != 0) read the row's last k-block and are
-    // zeroed when stored, so the loads carry no select that would wait for them.
-    // Waves without a fragment of their own reload the last one (branches
-    // around loads make the compiler wait for every load at the join).
+  auto load_w = [&](int kt, Stage& st) {
 #pragma unroll
-    for (int i = 0; i < FPT; ++i) {
-      const int f = min(wave + kWaves * i, NFRAG - 1);
-      const uint32_t k0 = (uint32_t)min(kt * 128 + (f & 3) * 32, a.K - 32);
-      st.xr[i] = ld_off<u32x4>(x, xrow[i] + (k0 + (uint32_t)lg * 8u) * 2u);
-    }
-#pragma unroll
-    for (int j = 0; j < TW; ++j) st.q[j] = ld_off_nt<u32x4>(we, woff[j] + (uint32_t)kt * 1024u);
+    for (int j = 0; j < TW; ++j) st.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kt * 1024, kCacheStream);
 #pragma unroll
     for (int gg = 0; gg < GPT; ++gg) {
-      const uint32_t g = (uint32_t)min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
+      const int g = min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
 #pragma unroll
       for (int j = 0; j < TW; ++j) {
-        const uint32_t gi = goff[j] + g;
-        st.z[j][gg] = ld_off<uint32_t>(ze, gi * 8u + (uint32_t)(c >> 3) * 4u);
-        st.s[j][gg] = ld_off<uint16_t>(se, (gi * 16u + c) * 2u);
+        st.z[j][gg] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j], g * 8, 0);
+        st.s[j][gg] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], g * 32, 0);
       }
     }
   };
-  auto store_x = [&](const Stage& st, int kt) {
-    u32x4* buf = xs + (kt & 1) * kXsBuf;
+  // One k-tile: the activation operands and dequantised weights of k-block
+  // w + 1 are fetched while k-block w's MFMAs run (operands double-buffered),
+  // so no MFMA waits for an LDS read or a dequantisation issued just before.
+  auto compute = [&](const Stage& st, const u32x4* buf) {
+    ZS zs[TW][GPT];
 #pragma unroll
-    for (int i = 0; i < FPT; ++i) {
-      const int f = wave + kWaves * i;
-      if (f < NFRAG) {
-        const bool kval = kt * 128 + (f & 3) * 32 < a.K;
-        buf[f * 64 + lane] = kval ? st.xr[i] : u32x4{0u, 0u, 0u, 0u};
+    for (int gg = 0; gg < GPT; ++gg)
+#pragma unroll
+      for (int j = 0; j < TW; ++j) zs[j][gg] = Dq<DT>::make((st.z[j][gg] >> (4 * (c & 7))) & 0xFu, st.s[j][gg]);
+    V8 av[2][TW], bx[2][MC];
+#pragma unroll
+    for (int mt = 0; mt < MC; ++mt) bx[0][mt] = __builtin_bit_cast(V8, buf[(mt * 4) * 64 + lane]);
+#pragma unroll
+    for (int j = 0; j < TW; ++j) av[0][j] = Dq<DT>::word(st.q[j][0], zs[j][0], dk);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {  // k-blocks past K meet zeroed activations
+      const int cur = w & 1, nxt = cur ^ 1;
+      if (w + 1 < 4) {
+#pragma unroll
+        for (int mt = 0; mt < MC; ++mt) bx[nxt][mt] = __builtin_bit_cast(V8, buf[(mt * 4 + w + 1) * 64 + lane]);
+#pragma unroll
+        for (int j = 0; j < TW; ++j) av[nxt][j] = Dq<DT>::word(st.q[j][w + 1], zs[j][(w + 1) / BPG], dk);
       }
-    }
-  };
-  auto compute = [&](const Stage& st, int kt) {
-    const u32x4* buf = xs + (kt & 1) * kXsBuf;
 #pragma unroll
-    for (int gg = 0; gg < GPT; ++gg) {
-      ZS zs[TW];
+      for (int mt = 0; mt < MC; ++mt)
 #pragma unroll
-      for (int j = 0; j < TW; ++j) zs[j] = Dq<DT>::make((st.z[j][gg] >> (4 * (c & 7))) & 0xFu, st.s[j][gg]);
+        for (int j = 0; j < TW; ++j) acc[mt][j] = mfma16x16x32(av[cur][j], bx[cur][mt], acc[mt][j]);
+      if (w + 1 < 4) {
+        // MC * TW MFMAs, MC LDS reads and 26 vector operations (two words'
+        // dequantisation) per k-block: spread the reads and the vector work
+        // between the MFMAs.
 #pragma unroll
-      for (int b = 0; b < BPG; ++b) {
-        const int w = gg * BPG + b;  // k-blocks past K meet zeroed activations
-        V8 av[TW];
-#pragma unroll
-        for (int j = 0; j < TW; ++j) av[j] = Dq<DT>::word(st.q[j][w], zs[j], dk);
-#pragma unroll
-        for (int mt = 0; mt < MC; ++mt) {
-          const V8 bx = __builtin_bit_cast(V8, buf[(mt * 4 + w) * 64 + lane]);
-#pragma unroll
-          for (int j = 0; j < TW; ++j) acc[mt][j] = mfma16x16x32(av[j], bx, acc[mt][j]);
+        for (int i = 0; i < MC * TW; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
+          if (i < MC) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // LDS read
+          __builtin_amdgcn_sched_group_barrier(0x002, (26 + MC * TW - 1) / (MC * TW), 0);  // VALU
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-  };
-  // One k-tile: prefetch tile kt + 2 (past the end the last tile reloads
-  // itself, so the loads are unconditional), compute tile kt, publish tile
-  // kt + 1's activations to the other LDS buffer.
-  auto step = [&](int kt, const Stage& cur, const Stage& nxt1, Stage& nxt2) {
-    load(min(kt + 2, a.KT - 1), nxt2);
-    // Keep the prefetch ahead of this tile's math (the scheduler would
-    // otherwise start the math first, waiting for this tile's loads while the
-    // later tiles' are not yet issued).
-    __builtin_amdgcn_sched_barrier(0);
-    compute(cur, kt);
-    store_x(nxt1, kt + 1);
-    __syncthreads();
   };
 
-  Stage s0, s1, s2;
-  load(0, s0);
-  load(min(1, a.KT - 1), s1);
-  store_x(s0, 0);
+  // Weights run NSt - 1 k-tiles ahead of the multiply.  The k loop is padded
+  // to a multiple of NSt and runs without a branch around any load or
+  // multiply, so each stage keeps its registers across iterations and the
+  // compiler's waits are the exact in-order counts (a conditional step makes
+  // it copy stage registers, and the copy waits for their loads): padding
+  // k-tiles reload the last weight k-tile and meet zero activations.  The
+  // first chunk's activations are loaded after the first weights are issued;
+  // at a chunk boundary the waves meet, the next chunk is loaded over the
+  // last one, and they meet again.
+  constexpr int NSt = NS;
+  constexpr int KCS = KC / NSt * NSt;  // chunk length in whole loop iterations
+  const int KTp = (KT + NSt - 1) / NSt * NSt;
+  Stage st[NSt];
+#pragma unroll
+  for (int p = 0; p + 1 < NSt; ++p) load_w(min(p, KT - 1), st[p]);
+  int kc0 = 0, kc1 = min(KCS, KTp);
+  load_chunk(kc0, kc1);
   __syncthreads();
-  for (int kt = 0; kt < a.KT; kt += 3) {
-    step(kt, s0, s1, s2);
-    if (kt + 1 < a.KT) step(kt + 1, s1, s2, s0);
-    if (kt + 2 < a.KT) step(kt + 2, s2, s0, s1);
+  for (int kt = 0; kt < KTp; kt += NSt) {
+#pragma unroll
+    for (int i = 0; i < NSt; ++i) {
+      load_w(min(kt + i + NSt - 1, KT - 1), st[(i + NSt - 1) % NSt]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's math
+      compute(st[i], xs + (kt + i - kc0) * MC * 4 * 64);
+    }
+    if (kt + NSt == kc1 && kc1 < KTp) {  // chunk boundary (workgroup-uniform; no stage registers change)
+      __syncthreads();
+      kc0 = kc1;
+      kc1 = min(kc1 + KCS, KTp);
+      load_chunk(kc0, kc1);
+      __syncthreads();
+    }
   }
 
   // Epilogue: lane (c, lg) of fragment (mt, j) holds row c of m-tile mt and
@@ -495,9 +532,9 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   }
 }
 
-template <int GPT, int EPI, typename DT>
+template <int GPT, int EPI, int NS, typename DT>
 __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
-  __shared__ u32x4 xs[kXsBufs * kXsBuf];
+  __shared__ u32x4 xs[kXsFrags * 64];
   // XCD-aware placement: workgroup b runs on XCD b % 8; logical index L
   // walks the column slices of one expert on one XCD.
   const int per = gridDim.x >> 3;
@@ -533,12 +570,12 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
   for (int p = blockIdx.y; p * kMaxMt < nblk; p += gridDim.y) {
     const int rb = r0 + p * kMaxMt * 16;
     switch (min(nblk - p * kMaxMt, kMaxMt)) {
-      case 1: moe_pass<1, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      case 2: moe_pass<2, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      case 3: moe_pass<3, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      default: moe_pass<4, GPT, EPI, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 1: moe_pass<1, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 2: moe_pass<2, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 3: moe_pass<3, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      default: moe_pass<4, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
     }
-    __syncthreads();  // the next pass refills both LDS buffers
+    __syncthreads();  // the next pass refills the activation chunk
   }
 }
 
@@ -571,15 +608,18 @@ template <typename DT>
 hipError_t launch_moe_gemm_dt(const MoeArgs& a, int gpt, int epi, int passes, hipStream_t s) {
   const int64_t gx = (a.total + 7) / 8 * 8;
   dim3 grid((unsigned)gx, (unsigned)passes);
-#define SGL_MOE(GPT_, EPI_)                                                                 \
-  if (gpt == GPT_ && epi == EPI_) {                                                         \
-    hipLaunchKernelGGL((moe_gemm_kernel<GPT_, EPI_, DT>), grid, dim3(kThreads), 0, s, a);   \
-    return hipGetLastError();                                                               \
+  const int ns = (gpt >= 4 || (a.KT % 4 != 0 && a.KT % 3 == 0)) ? 3 : 4;
+#define SGL_MOE(GPT_, EPI_, NS_)                                                                \
+  if (gpt == GPT_ && epi == EPI_ && ns == NS_) {                                                \
+    hipLaunchKernelGGL((moe_gemm_kernel<GPT_, EPI_, NS_, DT>), grid, dim3(kThreads), 0, s, a);  \
+    return hipGetLastError();                                                                   \
   }
-#define SGL_MOE_E(GPT_) SGL_MOE(GPT_, kEpiPlain) SGL_MOE(GPT_, kEpiSilu) SGL_MOE(GPT_, kEpiGelu)
-  SGL_MOE_E(1)
-  SGL_MOE_E(2)
-  SGL_MOE_E(4)
+#define SGL_MOE_E(GPT_, NS_) SGL_MOE(GPT_, kEpiPlain, NS_) SGL_MOE(GPT_, kEpiSilu, NS_) SGL_MOE(GPT_, kEpiGelu, NS_)
+  SGL_MOE_E(1, 4)
+  SGL_MOE_E(1, 3)
+  SGL_MOE_E(2, 4)
+  SGL_MOE_E(2, 3)
+  SGL_MOE_E(4, 3)
 #undef SGL_MOE_E
 #undef SGL_MOE
   return hipErrorInvalidValue;
