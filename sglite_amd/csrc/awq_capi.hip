@@ -515,6 +515,8 @@ int awq_moe_w4a16_gemm(const void* a, int64_t a_rows, const void* w, const void*
                 "awq_moe_w4a16_gemm: %lld routed rows with top_k %lld need %lld activation rows, a has %lld",
                 (long long)num_routed, (long long)top_k, (long long)((num_routed + top_k - 1) / top_k),
                 (long long)a_rows);
+  if ((num_routed + top_k - 1) / top_k * K * 2 >= (int64_t(1) << 31))
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_w4a16_gemm: the routed activation rows must span below 2 GiB");
   if (num_routed == 0 || sorted_cap == 0) return ok();
   if (!a || !w || !s || !z || !sorted_ids || !expert_offsets || !out || (mul_routed_weight && !topk_weights))
     return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_w4a16_gemm: null pointer argument");

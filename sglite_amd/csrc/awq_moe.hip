@@ -15,14 +15,15 @@
 //                             writing [T * k, H]    (second GEMM)
 //   moe_sum_kernel        out[t] = sum_j y[t * k + j] in fp32, cast once
 //
-// The grouped GEMM keeps a pass's gathered activation rows resident in LDS in
-// MFMA fragment order (up to 128 KiB) so the eight waves of a workgroup share
-// one copy and then run without meeting each other; each wave dequantises the
-// weights of its own 32 columns straight from global memory into MFMA
-// operands, several k-tiles ahead.  A workgroup
-// serves every block of one expert for its column slice, so each expert's
-// weights are streamed from HBM once per forward; workgroups of one expert are
-// placed on one XCD so the expert's activation rows are fetched into one L2.
+// The grouped GEMM streams a pass's gathered activation rows into a ring of
+// LDS slots in MFMA fragment order by LDS-DMA, as many k-tiles ahead as the
+// weights, so the four waves of a workgroup share one copy; each wave
+// dequantises the weights of its own 32 columns straight from global memory
+// into MFMA operands.  A workgroup runs several column slices of one expert
+// back to back in one load pipeline, and two workgroups share a CU, paired
+// heavy with light by their m-tile counts.  Each expert's weights are
+// streamed from HBM once per forward; workgroups of one expert are placed on
+// one XCD so the expert's activation rows are fetched into one L2.
 #include <math.h>
 
 #include <algorithm>
@@ -287,6 +288,7 @@ __device__ __forceinline__ float gate_act(float g) {
 
 struct MoeArgs {
   const void* x;           // activation rows [rows_in, K]
+  uint32_t x_bytes;        // rows_in * K * 2 (below 2^31: the host checks)
   const u32x4* wt;         // expert-stacked weight tiles
   const uint16_t* s_r;     // expert-stacked scales [E][NT][NG][16]
   const uint64_t* z_r;     // expert-stacked zero words [E][NT][NG]
@@ -298,47 +300,62 @@ struct MoeArgs {
   int num_routed, sorted_cap;
   int N, K, NT, KT, NG, gshift;
   int64_t w_stride, s_stride, z_stride;  // per-expert strides in u32x4 / scale / zero-word units
-  int S, total;  // column slices per expert, S * E
+  int S;      // column slices per expert
+  int U;      // slices per workgroup, run back to back in one pipeline
+  int SG;     // slice groups per expert, ceil(S / U)
+  int total;  // SG * E
+  int cpx;    // CUs per XCD
   int mul_rw;
 };
 
-// Workgroup shape: 8 waves (two per SIMD), each owning two 16-column tiles
-// (256 columns per workgroup, or 128 gate + 128 up columns with a gate/up
-// activation), so the gathered activation rows in LDS feed 16 tiles.
-constexpr int kWaves = 8;
+// Workgroup shape: 4 waves (one per SIMD), each owning TW = 2 16-column
+// tiles of a slice (128 columns per slice; with a gate/up activation a gate
+// tile and its up tile).  Two workgroups run on a CU; with eight waves in one
+// workgroup the younger wave of each SIMD finished its k loop microseconds
+// after the older one, alone on the SIMD.  (Four tiles per wave halve the
+// activation traffic per weight byte but need more than 256 VGPRs at four
+// m-tiles, and measured no faster.)  A workgroup runs U slices of one expert
+// back to back in one load pipeline (the next slice's first k-tiles are
+// fetched during the current slice's last ones), so the routed-row set-up and
+// the pipeline fill are paid once per workgroup; the host picks U for about
+// two workgroups per CU.
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTilesPerWave = 2;
 // Routed rows per pass: up to kMaxMt m-tiles of 16.  An expert with more rows
 // takes more passes, spread over grid.y so that they run side by side and
 // share the expert's weights through L2.
 constexpr int kMaxMt = 4;
-// The pass's activation rows stay resident in LDS for a chunk of k-tiles:
-// 128 KiB = 128 fragments of 1 KiB ([k-tile][m-tile][k-block][lane]), i.e.
-// up to 32 / MC k-tiles for MC m-tiles, in whole loop iterations (all of
-// K = 2048 at up to two m-tiles, all of K = 768 at four).  Within a chunk the
-// waves never wait for each other.
-constexpr int kXsFrags = 128;
+// The pass's activation rows reach LDS through a ring of k-tile slots of MC *
+// 4 fragments of 1 KiB ([slot][m-tile][k-block][lane]) within 80 KiB, filled
+// by LDS-DMA as many k-tiles ahead as the weights.
+constexpr int kXsFrags = 80;
 
 // Weight k-tiles held in registers per wave (NS: the one being multiplied and
-// NS - 1 in flight): the host picks 4, or 3 where K spans a multiple of three
-// k-tiles but not of four (the k loop is padded to a multiple of NS), and 3
-// with four quantisation groups per k-tile (their zero and scale words take
-// the registers).
+// NS - 1 in flight): with one quantisation group per k-tile the host picks 4,
+// or 3 where K spans a multiple of three k-tiles but not of four (the k loop
+// is padded to a multiple of NS); 3 with two groups per k-tile and 2 with four
+// (their zero and scale words take the registers).
 
-// One pass over K for MC m-tiles (16 routed rows each) starting at sorted row
-// rb.  The wave's column tiles are ntc[0..1] (expert-local tile indices).
-template <int MC, int GPT, int EPI, int NS, typename DT>
+// One pass over `units` slices (from slice u0) and all of K for MC m-tiles
+// (16 routed rows each) starting at sorted row rb.  Tile j of the wave in
+// slice u0 + u is tile0[j] + u * TSU of the expert (TSU = tiles per slice in
+// each half); tiles past the expert's last read as zeros (the buffer ranges
+// end there) and are never stored.
+template <int MC, int TW, int GPT, int EPI, int NS, typename DT>
 __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ xs, const u32x4* __restrict__ we,
                                          const uint16_t* __restrict__ se, const uint64_t* __restrict__ ze,
-                                         const int (&ntc)[kTilesPerWave], const int (&ncol)[kTilesPerWave], int rb,
-                                         int wave, int lane) {
+                                         const int (&tile0)[TW], int u0, int units, int rb, int wave, int lane) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
   using V4 = typename DT::vec4;
   using ZS = typename Dq<DT>::ZS;
-  constexpr int TW = kTilesPerWave;
-  constexpr int BPG = 4 / GPT;               // 32-row k-blocks per group
-  constexpr int KC = kXsFrags / (MC * 4);    // k-tiles per resident activation chunk
+  constexpr int BPG = 4 / GPT;      // 32-row k-blocks per group
+  constexpr int FR = MC * 4;        // activation fragments per k-tile
+  constexpr int R = kXsFrags / FR;  // ring slots
+  static_assert(R >= NS + 1, "the slot being filled must not be the one the slowest wave still reads");
+  constexpr int HT = EPI == kEpiPlain ? TW : TW / 2;  // tiles per wave in each half of a slice
+  constexpr int TSU = kWaves * HT;                     // slice stride in tiles
   const int c = lane & 15, lg = lane >> 4;
   const int KT = a.KT;
   const DqK dk = dq_consts();
@@ -348,41 +365,28 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   // output column m depends on activation row m only).
   int sid[MC];
   bool sval[MC];
-  uint32_t xrow[MC];  // byte offset of the lane's activation row (the host keeps `a` below 4 GiB)
+  uint32_t xrow[MC];  // byte offset of the lane's activation row (below x_bytes < 2^31)
+  float rw[MC];       // routed weight of the row, fetched now so the epilogue does not wait for it
 #pragma unroll
   for (int i = 0; i < MC; ++i) {
     sid[i] = a.sorted[rb + i * 16 + c];
     sval[i] = sid[i] >= 0 && sid[i] < a.num_routed;
     xrow[i] = (uint32_t)(sval[i] ? sid[i] / a.a_div : 0) * (uint32_t)a.K * 2u + (uint32_t)lg * 16u;
+    rw[i] = a.mul_rw && sval[i] ? a.topk_w[sid[i]] : 1.f;
   }
 
-  // Activation chunk [kc0, kc1) -> LDS: fragment f = (k-tile - kc0, m-tile,
-  // k-block) of 16 rows x 32 k, lane (c, lg) bringing row c's 8 elements at
-  // 8 lg.  Wave w takes fragments w, w + 8, ..., eight loads in flight before
-  // their LDS stores (a fragment index past the end repeats the last one).
-  // k-blocks past K store zeros.
-  auto load_chunk = [&](int kc0, int kc1) {
-    const int nf = (kc1 - kc0) * MC * 4;
-    for (int f0 = wave; f0 < nf; f0 += 8 * kWaves) {
-      u32x4 v[8];
+  // Activation k-tile kt -> ring slot by LDS-DMA: wave w brings k-block w of
+  // every m-tile (fragment (m-tile, w) of 16 rows x 32 k), lane (c, lg) row
+  // c's 8 elements at 8 lg, straight into slot position lane.  k-blocks past K
+  // (the K tail and the padding k-tiles) read at offset x_bytes, outside the
+  // buffer, which returns zeros.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
+  auto dma_x = [&](int kt, int slot) {
+    const int k0 = kt * 128 + wave * 32;
+    u32x4* dst = xs + slot * FR * 64;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int f = min(f0 + i * kWaves, nf - 1);
-        const int w = f & 3, mt = (f >> 2) % MC, kt = kc0 + (f >> 2) / MC;
-        uint32_t row = xrow[0];
-#pragma unroll
-        for (int q = 1; q < MC; ++q)
-          if (mt == q) row = xrow[q];
-        const uint32_t k0 = (uint32_t)min(kt * 128 + w * 32, a.K - 32);
-        v[i] = ld_off<u32x4>(a.x, row + k0 * 2u);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int f = min(f0 + i * kWaves, nf - 1);
-        const int w = f & 3, kt = kc0 + (f >> 2) / MC;
-        xs[f * 64 + lane] = kt * 128 + w * 32 < a.K ? v[i] : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
+    for (int mt = 0; mt < MC; ++mt)
+      load_lds16(xr, dst + (mt * 4 + wave) * 64, k0 < a.K ? xrow[mt] + (uint32_t)k0 * 2u : a.x_bytes, 0);
   };
 
   f32x4 acc[MC][TW];
@@ -391,36 +395,42 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
 #pragma unroll
     for (int j = 0; j < TW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // The expert's weights, zero words and scales as buffer resources (explicit
-  // global loads with the k-tile and group offsets in scalar registers);
-  // per-tile byte offsets inside them.
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(we, (uint32_t)(a.w_stride * 16));
-  const __amdgpu_buffer_rsrc_t zr = make_rsrc(ze, (uint32_t)(a.z_stride * 8));
-  const __amdgpu_buffer_rsrc_t sr = make_rsrc(se, (uint32_t)(a.s_stride * 2));
+  // The expert's weights, zero words and scales as buffer resources that end
+  // at its last tile (explicit global loads with the slice, k-tile and group
+  // offsets in scalar registers); per-lane byte offsets of the wave's tiles
+  // in the first slice.
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(we, (uint32_t)a.NT * (uint32_t)KT * 1024u);
+  const __amdgpu_buffer_rsrc_t zr = make_rsrc(ze, (uint32_t)a.NT * (uint32_t)a.NG * 8u);
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(se, (uint32_t)a.NT * (uint32_t)a.NG * 32u);
+  const uint32_t wsh = (uint32_t)TSU * (uint32_t)KT * 1024u;  // per-slice shifts
+  const uint32_t zsh = (uint32_t)TSU * (uint32_t)a.NG * 8u;
+  const uint32_t ssh = (uint32_t)TSU * (uint32_t)a.NG * 32u;
   uint32_t woff[TW], zoff[TW], soff[TW];
 #pragma unroll
   for (int j = 0; j < TW; ++j) {
-    woff[j] = ((uint32_t)ntc[j] * (uint32_t)KT * 64u + lane) * 16u;
-    zoff[j] = (uint32_t)ntc[j] * (uint32_t)a.NG * 8u + (uint32_t)(c >> 3) * 4u;
-    soff[j] = ((uint32_t)ntc[j] * (uint32_t)a.NG * 16u + (uint32_t)c) * 2u;
+    const uint32_t t = (uint32_t)(tile0[j] + u0 * TSU);
+    woff[j] = (t * (uint32_t)KT * 64u + lane) * 16u;
+    zoff[j] = t * (uint32_t)a.NG * 8u + (uint32_t)(c >> 3) * 4u;
+    soff[j] = (t * (uint32_t)a.NG * 16u + (uint32_t)c) * 2u;
   }
 
-  // A k-tile's weights, zero points and scales for the wave's two tiles.
+  // A k-tile's weights, zero points and scales for the wave's tiles.
   struct Stage {
     u32x4 q[TW];          // weight words of the wave's column tiles
     uint32_t z[TW][GPT];  // zero-point word holding the lane's nibble
     uint16_t s[TW][GPT];  // scale bits (kept 16-bit: a widening would wait for the load at once)
   };
-  auto load_w = [&](int kt, Stage& st) {
+  auto load_w = [&](int u, int kt, Stage& st) {
 #pragma unroll
-    for (int j = 0; j < TW; ++j) st.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], kt * 1024, kCacheStream);
+    for (int j = 0; j < TW; ++j)
+      st.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], u * wsh + kt * 1024, kCacheStream);
 #pragma unroll
     for (int gg = 0; gg < GPT; ++gg) {
       const int g = min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
 #pragma unroll
       for (int j = 0; j < TW; ++j) {
-        st.z[j][gg] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j], g * 8, 0);
-        st.s[j][gg] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], g * 32, 0);
+        st.z[j][gg] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j], u * zsh + g * 8, 0);
+        st.s[j][gg] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], u * ssh + g * 32, 0);
       }
     }
   };
@@ -452,116 +462,192 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
 #pragma unroll
         for (int j = 0; j < TW; ++j) acc[mt][j] = mfma16x16x32(av[cur][j], bx[cur][mt], acc[mt][j]);
       if (w + 1 < 4) {
-        // MC * TW MFMAs, MC LDS reads and 26 vector operations (two words'
-        // dequantisation) per k-block: spread the reads and the vector work
-        // between the MFMAs.
+        // MC * TW MFMAs, MC LDS reads and 13 * TW vector operations (TW
+        // words' dequantisation) per k-block: spread the reads and the
+        // vector work between the MFMAs.
 #pragma unroll
         for (int i = 0; i < MC * TW; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // MFMA
           if (i < MC) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // LDS read
-          __builtin_amdgcn_sched_group_barrier(0x002, (26 + MC * TW - 1) / (MC * TW), 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x002, (13 * TW + MC * TW - 1) / (MC * TW), 0);  // VALU
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
 
-  // Weights run NSt - 1 k-tiles ahead of the multiply.  The k loop is padded
-  // to a multiple of NSt and runs without a branch around any load or
-  // multiply, so each stage keeps its registers across iterations and the
-  // compiler's waits are the exact in-order counts (a conditional step makes
-  // it copy stage registers, and the copy waits for their loads): padding
-  // k-tiles reload the last weight k-tile and meet zero activations.  The
-  // first chunk's activations are loaded after the first weights are issued;
-  // at a chunk boundary the waves meet, the next chunk is loaded over the
-  // last one, and they meet again.
-  constexpr int NSt = NS;
-  constexpr int KCS = KC / NSt * NSt;  // chunk length in whole loop iterations
-  const int KTp = (KT + NSt - 1) / NSt * NSt;
-  Stage st[NSt];
-#pragma unroll
-  for (int p = 0; p + 1 < NSt; ++p) load_w(min(p, KT - 1), st[p]);
-  int kc0 = 0, kc1 = min(KCS, KTp);
-  load_chunk(kc0, kc1);
-  __syncthreads();
-  for (int kt = 0; kt < KTp; kt += NSt) {
-#pragma unroll
-    for (int i = 0; i < NSt; ++i) {
-      load_w(min(kt + i + NSt - 1, KT - 1), st[(i + NSt - 1) % NSt]);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's math
-      compute(st[i], xs + (kt + i - kc0) * MC * 4 * 64);
-    }
-    if (kt + NSt == kc1 && kc1 < KTp) {  // chunk boundary (workgroup-uniform; no stage registers change)
-      __syncthreads();
-      kc0 = kc1;
-      kc1 = min(kc1 + KCS, KTp);
-      load_chunk(kc0, kc1);
-      __syncthreads();
-    }
-  }
-
-  // Epilogue: lane (c, lg) of fragment (mt, j) holds row c of m-tile mt and
-  // columns 4lg..4lg+3 of tile j.
+  // Epilogue of slice u: lane (c, lg) of fragment (mt, j) holds row c of
+  // m-tile mt and columns 4lg..4lg+3 of tile j.
   E* out = (E*)a.out;
+  auto epilogue = [&](int u) {
 #pragma unroll
-  for (int mt = 0; mt < MC; ++mt) {
-    if (!sval[mt]) continue;
-    const float rw = a.mul_rw ? a.topk_w[sid[mt]] : 1.f;
-    if constexpr (EPI == kEpiPlain) {
+    for (int mt = 0; mt < MC; ++mt) {
+      if (!sval[mt]) continue;
+      if constexpr (EPI == kEpiPlain) {
 #pragma unroll
-      for (int j = 0; j < TW; ++j) {
-        if (ncol[j] < 0 || ncol[j] + 4 * lg >= a.N) continue;  // N % 16 == 8: half of the last tile
-        V4 r;
+        for (int j = 0; j < TW; ++j) {
+          const int nt = tile0[j] + (u0 + u) * TSU;
+          if (nt >= a.NT || nt * 16 + 4 * lg >= a.N) continue;  // N % 16 == 8: half of the last tile
+          V4 r;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = (E)(acc[mt][j][i] * rw);
-        *(V4*)(out + (int64_t)sid[mt] * a.N + ncol[j] + 4 * lg) = r;
+          for (int i = 0; i < 4; ++i) r[i] = (E)(acc[mt][j][i] * rw[mt]);
+          *(V4*)(out + (int64_t)sid[mt] * a.N + nt * 16 + 4 * lg) = r;
+        }
+      } else {
+        // Tiles 0 .. TW/2 - 1 are gate tiles and tile j + TW/2 the up tile of
+        // gate tile j; the first GEMM's output is rounded before the
+        // activation (fused.py:175-177).
+#pragma unroll
+        for (int j = 0; j < HT; ++j) {
+          const int gt = tile0[j] + (u0 + u) * TSU;
+          if (gt >= (a.NT >> 1)) continue;
+          V4 r;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = (float)(E)(acc[mt][j][i] * rw[mt]);
+            const float v = (float)(E)(acc[mt][j + HT][i] * rw[mt]);
+            r[i] = (E)(gate_act<EPI>(g) * v);
+          }
+          *(V4*)(out + (int64_t)sid[mt] * (a.N >> 1) + gt * 16 + 4 * lg) = r;
+        }
       }
-    } else {
-      // Tile 0 is a gate tile and tile 1 the matching up tile; the first
-      // GEMM's output is rounded before the activation (fused.py:175-177).
-      if (ncol[0] < 0) continue;
-      V4 r;
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float g = (float)(E)(acc[mt][0][i] * rw);
-        const float u = (float)(E)(acc[mt][1][i] * rw);
-        r[i] = (E)(gate_act<EPI>(g) * u);
-      }
-      *(V4*)(out + (int64_t)sid[mt] * (a.N >> 1) + ncol[0] + 4 * lg) = r;
+    for (int mt = 0; mt < MC; ++mt)
+#pragma unroll
+      for (int j = 0; j < TW; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  // The steps run over (slice, k-tile), k-tiles padded to KTp (a multiple of
+  // NS); activations and weights run NS - 1 steps ahead of the multiply: each
+  // step issues the activation DMA and then the weight loads of step
+  // s + NS - 1 (the next slice's first k-tiles during this slice's last
+  // ones), waits until its own loads of step s (and everything older) have
+  // landed -- all but the NS - 1 newer steps' loads, the loads completing in
+  // order -- and meets the other waves at a barrier, after which every wave's
+  // DMA share of step s is in LDS.  The slot filled at step s held step
+  // s + NS - 1 - R <= s - 2, which every wave finished before the previous
+  // step's barrier.  The barrier is a bare s_barrier: a fence would wait for
+  // all loads and drain the pipeline.  The loop runs without a branch around
+  // any load or multiply, so each stage keeps its registers across iterations
+  // and the compiler's waits are the exact in-order counts (a conditional step
+  // makes it copy stage registers, and the copy waits for their loads):
+  // padding k-tiles reload the last weight k-tile and meet zero activations,
+  // and the steps past the last slice load what the buffer ranges allow and
+  // are never multiplied.  A slice's epilogue runs between loop iterations
+  // (its stores only make later waits stricter).
+  constexpr int LW = TW * (1 + 2 * GPT);           // weight, zero and scale loads per k-tile
+  constexpr int kInFlight = (NS - 1) * (MC + LW);  // loads of the NS - 1 newer steps
+  static_assert(kInFlight <= 63, "vmcnt holds at most 63");
+  const int KTp = (KT + NS - 1) / NS * NS;
+  const int nsteps = units * KTp;
+  int iu = 0, ik = 0, islot = 0;  // next step to issue: slice, k-tile, ring slot
+  auto issue = [&](Stage& st) {
+    dma_x(ik, islot);
+    load_w(iu, min(ik, KT - 1), st);
+    islot = islot + 1 == R ? 0 : islot + 1;
+    ik = ik + 1 == KTp ? 0 : ik + 1;
+    iu = ik == 0 ? iu + 1 : iu;
+  };
+  Stage st[NS];
+  // The prologue issues in the steady-state order (an empty asm statement
+  // with a memory clobber keeps the compiler from grouping the loads by
+  // kind), so the waits the compiler derives for the loop hold from its first
+  // step.
+#pragma unroll
+  for (int p = 0; p + 1 < NS; ++p) {
+    issue(st[p]);
+    __asm__ volatile("" ::: "memory");
+  }
+  int cu = 0, ck = 0, cslot = 0;  // step being multiplied
+  for (int s = 0; s < nsteps; s += NS) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      issue(st[(i + NS - 1) % NS]);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's math
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kInFlight));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      compute(st[i], xs + cslot * FR * 64);
+      cslot = cslot + 1 == R ? 0 : cslot + 1;
+    }
+    ck += NS;
+    if (ck == KTp) {  // workgroup-uniform; no stage registers change
+      epilogue(cu);
+      ck = 0;
+      ++cu;
     }
   }
 }
 
-template <int GPT, int EPI, int NS, typename DT>
-__global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
+// Balanced placement of the slice groups of one XCD.  Launched on an idle
+// device, workgroup b runs on XCD b % 8 as the j-th (j = b / 8) of that XCD,
+// and local indices j and j + cpx share a CU.  A group's time grows with its
+// pass's m-tile count (per slice ~5.6 + 1.7 * m-tiles us of a CU shared by two
+// workgroups), so the XCD's groups are ranked by m-tile count, heaviest first,
+// and the j-th heaviest shares a CU with the j-th lightest instead of two
+// heavy groups meeting on one CU by chance.  Each wave ranks the groups
+// itself (one lane per group, ballots); the result is the logical group
+// index, or -1 for a local index with no group.  Placement other than assumed
+// changes only the balance, never the result.
+__device__ __forceinline__ int balanced_group(const MoeArgs& a, int xcd, int per, int j, int lane) {
+  const int L = xcd * per + lane;
+  int key = -1;  // lanes past the XCD's groups take no rank
+  if (lane < per) {
+    key = 0;
+    if (L < a.total) {
+      const int e = L / a.SG;
+      const int r0 = min(max(a.offsets[e], 0), a.sorted_cap);
+      const int r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
+      key = min((r1 - r0) >> 4, kMaxMt);
+    }
+  }
+  int rank = 0;
+#pragma unroll
+  for (int v = kMaxMt; v >= 0; --v) {
+    const uint64_t m = __ballot(key == v);
+    if (key == v) rank += __popcll(m & lanes_below(lane));
+    else if (key < v) rank += __popcll(m);
+  }
+  const int r = j < a.cpx ? j : per - 1 - (j - a.cpx);
+  const uint64_t hit = __ballot(key >= 0 && rank == r);
+  return hit ? xcd * per + __builtin_ctzll(hit) : -1;
+}
+
+template <int TW, int GPT, int EPI, int NS, typename DT>
+__global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
   __shared__ u32x4 xs[kXsFrags * 64];
   // XCD-aware placement: workgroup b runs on XCD b % 8; logical index L
-  // walks the column slices of one expert on one XCD.
-  const int per = gridDim.x >> 3;
-  const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (L >= a.total) return;
-  const int e = L / a.S, slice = L % a.S;
+  // walks the slice groups of one expert on one XCD.  With one pass per
+  // expert and between one and two workgroups per CU the groups of an XCD are
+  // paired heavy with light on its CUs.
+  const int per = gridDim.x >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int lane = threadIdx.x & 63;
+  const int L = gridDim.y == 1 && per > a.cpx && per <= 2 * a.cpx && per <= 64
+                    ? balanced_group(a, xcd, per, j, lane)
+                    : xcd * per + j;
+  if (L < 0 || L >= a.total) return;
+  const int e = L / a.SG, grp = L % a.SG;
+  const int u0 = grp * a.U, units = min(a.U, a.S - u0);
   const int r0 = min(max(a.offsets[e], 0), a.sorted_cap);
   const int r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
   const int nblk = (r1 - r0) >> 4;
   if ((int)blockIdx.y * kMaxMt >= nblk) return;
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  int ntc[kTilesPerWave], ncol[kTilesPerWave];
+  const int wave = threadIdx.x >> 6;
+  // Tiles of the wave in slice 0: TW consecutive tiles, or TW / 2 gate tiles
+  // and their up tiles (up tile of gate tile t is t + NT / 2).
+  int tile0[TW];
   if constexpr (EPI == kEpiPlain) {
 #pragma unroll
-    for (int j = 0; j < kTilesPerWave; ++j) {
-      const int nt = (slice * kWaves + wave) * kTilesPerWave + j;
-      ntc[j] = min(nt, a.NT - 1);
-      ncol[j] = nt < a.NT ? nt * 16 : -1;
-    }
+    for (int j = 0; j < TW; ++j) tile0[j] = wave * TW + j;
   } else {
-    const int NTg = a.NT >> 1;  // gate tiles; up tile of gate tile t is t + NTg
-    const int gt = slice * kWaves + wave;
-    ntc[0] = min(gt, NTg - 1);
-    ntc[1] = ntc[0] + NTg;
-    ncol[0] = gt < NTg ? gt * 16 : -1;
-    ncol[1] = -1;
+    constexpr int HT = TW / 2;
+#pragma unroll
+    for (int j = 0; j < HT; ++j) {
+      tile0[j] = wave * HT + j;
+      tile0[j + HT] = tile0[j] + (a.NT >> 1);
+    }
   }
   const u32x4* we = a.wt + e * a.w_stride;
   const uint16_t* se = a.s_r + e * a.s_stride;
@@ -570,12 +656,14 @@ __global__ __launch_bounds__(kThreads) void moe_gemm_kernel(MoeArgs a) {
   for (int p = blockIdx.y; p * kMaxMt < nblk; p += gridDim.y) {
     const int rb = r0 + p * kMaxMt * 16;
     switch (min(nblk - p * kMaxMt, kMaxMt)) {
-      case 1: moe_pass<1, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      case 2: moe_pass<2, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      case 3: moe_pass<3, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
-      default: moe_pass<4, GPT, EPI, NS, DT>(a, xs, we, se, ze, ntc, ncol, rb, wave, lane); break;
+      case 1: moe_pass<1, TW, GPT, EPI, NS, DT>(a, xs, we, se, ze, tile0, u0, units, rb, wave, lane); break;
+      case 2: moe_pass<2, TW, GPT, EPI, NS, DT>(a, xs, we, se, ze, tile0, u0, units, rb, wave, lane); break;
+      case 3: moe_pass<3, TW, GPT, EPI, NS, DT>(a, xs, we, se, ze, tile0, u0, units, rb, wave, lane); break;
+      default: moe_pass<4, TW, GPT, EPI, NS, DT>(a, xs, we, se, ze, tile0, u0, units, rb, wave, lane); break;
     }
-    __syncthreads();  // the next pass refills the activation chunk
+    // The last steps' DMAs and loads (past the last slice) land before the
+    // next pass reuses the ring or the workgroup ends (the fence waits for them).
+    __syncthreads();
   }
 }
 
@@ -605,21 +693,21 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const typename DT::elem* _
 }
 
 template <typename DT>
-hipError_t launch_moe_gemm_dt(const MoeArgs& a, int gpt, int epi, int passes, hipStream_t s) {
+hipError_t launch_moe_gemm_dt(const MoeArgs& a, int tw, int gpt, int epi, int passes, hipStream_t s) {
   const int64_t gx = (a.total + 7) / 8 * 8;
   dim3 grid((unsigned)gx, (unsigned)passes);
-  const int ns = (gpt >= 4 || (a.KT % 4 != 0 && a.KT % 3 == 0)) ? 3 : 4;
-#define SGL_MOE(GPT_, EPI_, NS_)                                                                \
-  if (gpt == GPT_ && epi == EPI_ && ns == NS_) {                                                \
-    hipLaunchKernelGGL((moe_gemm_kernel<GPT_, EPI_, NS_, DT>), grid, dim3(kThreads), 0, s, a);  \
-    return hipGetLastError();                                                                   \
+  const int ns = gpt >= 4 ? 2 : gpt == 2 ? 3 : (a.KT % 4 != 0 && a.KT % 3 == 0) ? 3 : 4;
+#define SGL_MOE(TW_, GPT_, EPI_, NS_)                                                                \
+  if (tw == TW_ && gpt == GPT_ && epi == EPI_ && ns == NS_) {                                        \
+    hipLaunchKernelGGL((moe_gemm_kernel<TW_, GPT_, EPI_, NS_, DT>), grid, dim3(kThreads), 0, s, a);  \
+    return hipGetLastError();                                                                        \
   }
-#define SGL_MOE_E(GPT_, NS_) SGL_MOE(GPT_, kEpiPlain, NS_) SGL_MOE(GPT_, kEpiSilu, NS_) SGL_MOE(GPT_, kEpiGelu, NS_)
-  SGL_MOE_E(1, 4)
-  SGL_MOE_E(1, 3)
-  SGL_MOE_E(2, 4)
-  SGL_MOE_E(2, 3)
-  SGL_MOE_E(4, 3)
+#define SGL_MOE_E(TW_, GPT_, NS_) \
+  SGL_MOE(TW_, GPT_, kEpiPlain, NS_) SGL_MOE(TW_, GPT_, kEpiSilu, NS_) SGL_MOE(TW_, GPT_, kEpiGelu, NS_)
+  SGL_MOE_E(2, 1, 4)
+  SGL_MOE_E(2, 1, 3)
+  SGL_MOE_E(2, 2, 3)
+  SGL_MOE_E(2, 4, 2)
 #undef SGL_MOE_E
 #undef SGL_MOE
   return hipErrorInvalidValue;
@@ -655,6 +743,7 @@ hipError_t launch_moe_align(const int32_t* ids, int64_t n, int64_t E, int64_t bs
 hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s) {
   MoeArgs a{};
   a.x = p.x;
+  a.x_bytes = (uint32_t)((p.num_routed + p.a_div - 1) / p.a_div * p.g.K * 2);
   a.wt = (const u32x4*)p.w;
   a.s_r = (const uint16_t*)p.s;
   a.z_r = (const uint64_t*)p.z;
@@ -675,17 +764,25 @@ hipError_t launch_moe_gemm(const MoeGemmParams& p, hipStream_t s) {
   a.w_stride = st.w / 16;
   a.s_stride = st.s / 2;
   a.z_stride = st.z / 8;
-  a.S = p.epi == kEpiPlain ? (int)((p.g.NT + kWaves * kTilesPerWave - 1) / (kWaves * kTilesPerWave))
-                            : (int)((p.g.NT / 2 + kWaves - 1) / kWaves);
-  a.total = a.S * (int)p.E;
+  const int tw = kTilesPerWave;
+  a.S = p.epi == kEpiPlain ? (int)((p.g.NT + kWaves * tw - 1) / (kWaves * tw))
+                            : (int)((p.g.NT / 2 + kWaves * tw / 2 - 1) / (kWaves * tw / 2));
   a.mul_rw = p.mul_rw;
   const int gpt = (p.g.NG > 1 && p.g.G < 128) ? (int)(128 / p.g.G) : 1;
   // Passes per expert side by side: enough for an expert with the average
   // number of routed rows plus half a block of padding.
   const int64_t avg_rows = p.num_routed / p.E + 8;
-  const int passes = (int)std::min<int64_t>(std::max<int64_t>((avg_rows + 16 * kMaxMt - 1) / (16 * kMaxMt), 1), 256);
-  return p.dtype == 0 ? launch_moe_gemm_dt<F16>(a, gpt, p.epi, passes, s)
-                      : launch_moe_gemm_dt<BF16>(a, gpt, p.epi, passes, s);
+  const int passes =
+      (int)std::min<int64_t>(std::max<int64_t>((avg_rows + 16 * kMaxMt - 1) / (16 * kMaxMt), 1), 256);
+  // Slices per workgroup: about two workgroups per CU over the grid.
+  const int64_t units_total = (int64_t)a.S * p.E * passes;
+  const int64_t cus = device_cu_count();
+  a.U = (int)std::min<int64_t>(std::max<int64_t>((units_total + 2 * cus - 1) / (2 * cus), 1), a.S);
+  a.cpx = (int)std::max<int64_t>(cus / 8, 1);
+  a.SG = (a.S + a.U - 1) / a.U;
+  a.total = a.SG * (int)p.E;
+  return p.dtype == 0 ? launch_moe_gemm_dt<F16>(a, tw, gpt, p.epi, passes, s)
+                      : launch_moe_gemm_dt<BF16>(a, tw, gpt, p.epi, passes, s);
 }
 
 hipError_t launch_moe_sum(const void* in, void* out, int64_t T, int64_t k, int64_t H, int dtype, hipStream_t s) {

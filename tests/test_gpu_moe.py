@@ -151,6 +151,48 @@ def test_grouped_gemm_skewed_routing_multi_pass(dtype):
         assert ok, (act, err, mx)
 
 
+def _uneven_ids(T, E, k, seed):
+    """Distinct experts per token: experts 0-3 take a fifth of the rows (about
+    T / 5 each: at T = 512 more than the 64 rows of one pass), experts 4-99 the
+    rest and experts 100 and above none."""
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.empty((T, k), dtype=torch.int32)
+    for t in range(T):
+        pick = torch.randperm(96, generator=g)[:k] + 4
+        if torch.rand(1, generator=g).item() < 0.8:
+            pick[0] = t % 4
+        ids[t] = pick.to(torch.int32)
+    return ids
+
+
+@pytest.mark.parametrize("N,activation", [(2048, None), (1928, None), (2048, "silu"), (2016, "gelu")])
+def test_grouped_gemm_balanced_placement_uneven_routing(N, activation):
+    """128 experts at about two workgroups per CU (the heavy/light pairing of
+    an XCD's slice groups), with experts of no rows, experts of more than one
+    pass and a partial last slice; every routed row of the NaN-filled output
+    is written and matches the oracle."""
+    ops = _ops()
+    T, E, k, K, G = 512, 128, 4, 256, 128
+    W = _experts(E, K, N, G, seed=N + 3)
+    ids = _uneven_ids(T, E, k, seed=N)
+    tw = torch.rand(ids.shape, generator=torch.Generator().manual_seed(9))
+    x = oracle.make_activation(T, K, seed=10)
+    d = _to_dev(W)
+    ex = ops.repack_experts(d["qweight"], d["qzeros"], d["scales"])
+    align = ops.moe_align_block_size(ids.to(DEV), 16, E)
+    counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
+    assert int(counts[:4].min()) > 64 and int(counts[100:].sum()) == 0
+    ncols = N // 2 if activation else N
+    out = torch.full((T * k, ncols), float("nan"), dtype=torch.float16, device=DEV)
+    mul = activation is None
+    ops.moe_gemm(x.to(DEV), ex, K, N, G, align, tw.to(DEV), T * k, k, activation, mul, out=out)
+    ref = oracle.moe_grouped_gemm(x, W, tw, ids, k, G, activation, mul)
+    got = out.cpu()
+    assert not torch.isnan(got).any()
+    ok, err, mx = oracle.tolerance_ok(got, ref, TOL)
+    assert ok, (err, mx)
+
+
 def test_grouped_gemm_block_size_32_alignment():
     """Buckets padded to 32 rows (a coarser alignment) give the same rows."""
     ops = _ops()
