@@ -344,15 +344,16 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // Row-block codes: 32, 64, 128 = tiled_kernel (16x16x32 MFMAs);
     // 1064, 1128 = mfma32_kernel (32x32x16 MFMAs) at 64 and 128 rows;
     // 2064, 2128 = the same with registers for two workgroups per CU;
-    // 4032 = the same at 32 rows with registers for four.
+    // 4032 = the same at 32 rows with registers for four;
+    // 8064, 8128 = 8 waves and 512 columns per workgroup, one per CU.
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
-                           env_bm == 2064 || env_bm == 2128 || env_bm == 4032;
+                           env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128;
     const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032}) {
+    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128}) {
       const int bm = code % 1000;
       if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
       if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
@@ -390,8 +391,19 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64 &&
         ((g.NT + 15) / 16) * ((g.M + 127) / 128) * 2 >= 3 * (int64_t)g.cus)
       best_bm = 2128;
+    // One 8-wave workgroup of 512 columns per CU instead of two of 256: the
+    // CU's columns share one activation stage (half the activation loads
+    // per weight byte), and a grid of at most one round, or of whole rounds,
+    // of 512-column tiles keeps every CU equally loaded where 256-column
+    // tiles would double up on some CUs only (Llama-3-8B qkv at M = 2048:
+    // 129 -> 112 us; qkv, o and down at M = 8192: 2-3% faster; gate_up at
+    // M = 2048, 3.5 rounds, stays faster with two workgroups per CU).
+    if (!env_bm_ok && best_bm == 2128 && g.G >= 128) {
+      const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 127) / 128);
+      if (t8 <= g.cus || t8 % g.cus == 0) best_bm = 8128;
+    }
     p.variant = best_bm;
-    p.grid_x = (g.NT + 15) / 16;
+    p.grid_x = best_bm >= 8000 ? (g.NT + 31) / 32 : (g.NT + 15) / 16;
     p.grid_y = (g.M + best_bm % 1000 - 1) / (best_bm % 1000);
     p.ktc = (int)((g.KT + ks - 1) / ks);
     p.ks = (int)((g.KT + p.ktc - 1) / p.ktc);  // every slice gets >= 1 k-tile
@@ -401,7 +413,8 @@ GemmPlan plan_gemm(const Geom& g, int act) {
 }
 
 int plan_threads(const GemmPlan& p) {
-  if (p.kind == 1 || p.kind == 3) return 256;
+  if (p.kind == 1) return p.variant >= 8000 ? 512 : 256;
+  if (p.kind == 3) return 256;
   if (p.kind == 2) return 64 * ((p.variant / 1000) % 10) * ((p.variant / 10) % 100);
   return 64 * ((p.variant / 100) % 100) * (p.variant % 100);
 }

@@ -417,7 +417,8 @@ hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, 
 // ---------------------------------------------------------------------------
 // 32x32 prefill kernel (v_mfma_f32_32x32x16).
 //
-// Same workgroup tile (BM x 256, 4 waves of 64 columns), pipeline and split-K
+// Same workgroup tile (BM x 256, 4 waves of 64 columns; or BM x 512 with 8
+// waves, whose columns share one activation stage), pipeline and split-K
 // scheme as tiled_kernel, but every MFMA is a 32x32x16 one: twice the work of
 // a 16x16x32 MFMA per issued instruction, so per k-tile a wave issues half the
 // MFMAs and the same dequantisation and LDS reads, leaving more issue slots for
@@ -433,14 +434,15 @@ hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, 
 // output columns 8 j + 4 (l / 32) .. + 3 (j = 0..3) of its column group.
 // ---------------------------------------------------------------------------
 
-template <int BM, int GPT, int NS, int OCC, typename DT>
-__global__ __launch_bounds__(256, OCC) void mfma32_kernel(TiledArgs a) {
+template <int BM, int GPT, int NS, int OCC, int NW, typename DT>
+__global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
   using ZS = typename Dq<DT>::ZS;
   constexpr int MT = BM / 32;              // m32 tiles
   constexpr int XF = MT * 8;               // activation fragments (1 KiB) per k-tile
-  constexpr int XPW = XF / 4;              // ... loaded by each wave
+  static_assert(XF % NW == 0, "whole activation fragments per wave");
+  constexpr int XPW = XF / NW;             // ... loaded by each wave
   constexpr int kLoadsW = 4 + 4 * GPT;     // weight-stage load instructions per k-tile
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
   static_assert(kAfterX < 64, "vector-memory counter range");
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(256, OCC) void mfma32_kernel(TiledArgs a) {
   // Weights of the wave's two column groups: group g covers slots 2g, 2g + 1
   // (with a fused gate/up activation: gate tiles t, t + 1 in group 0 and their
   // up tiles in group 1).  Tiles past the end clamp to the last tile.
-  const int nt0 = bx * 16 + wave * 4;
+  const int nt0 = bx * (4 * NW) + wave * 4;
   const int NTg = a.NT >> 1;
   const int pb0 = a.act ? (nt0 >> 1) : nt0;
   const int pb1 = a.act ? (nt0 >> 1) + NTg : nt0 + 2;
@@ -670,14 +672,15 @@ __global__ __launch_bounds__(256, OCC) void mfma32_kernel(TiledArgs a) {
 }
 
 // OCC = workgroups per CU the register budget is cut for (2: 256 registers,
-// two waves per SIMD, each workgroup's activation stages in 64 KiB of LDS).
-template <int BM, int NS, int OCC, typename DT>
+// two waves per SIMD, each workgroup's activation stages in 64 KiB of LDS);
+// NW = waves per workgroup (64 * NW columns).
+template <int BM, int NS, int OCC, int NW, typename DT>
 hipError_t launch_bm32(const TiledArgs& a, int gpt, hipStream_t s) {
-  const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(256);
+  const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(64 * NW);
   switch (gpt) {
-    case 1: hipLaunchKernelGGL((mfma32_kernel<BM, 1, NS, OCC, DT>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((mfma32_kernel<BM, 2, NS, OCC, DT>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((mfma32_kernel<BM, 4, 2, OCC, DT>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((mfma32_kernel<BM, 1, NS, OCC, NW, DT>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((mfma32_kernel<BM, 2, NS, OCC, NW, DT>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((mfma32_kernel<BM, 4, 2, OCC, NW, DT>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -702,11 +705,13 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
     case 32: return launch_bm<32, DT>(a, gpt, s);
     case 64: return launch_bm<64, DT>(a, gpt, s);
     case 128: return launch_bm<128, DT>(a, gpt, s);
-    case 1064: return launch_bm32<64, 3, 1, DT>(a, gpt, s);
-    case 1128: return launch_bm32<128, 3, 1, DT>(a, gpt, s);
-    case 2064: return launch_bm32<64, 3, 2, DT>(a, gpt, s);
-    case 2128: return launch_bm32<128, 2, 2, DT>(a, gpt, s);
-    case 4032: return launch_bm32<32, 3, 4, DT>(a, gpt, s);
+    case 1064: return launch_bm32<64, 3, 1, 4, DT>(a, gpt, s);
+    case 1128: return launch_bm32<128, 3, 1, 4, DT>(a, gpt, s);
+    case 2064: return launch_bm32<64, 3, 2, 4, DT>(a, gpt, s);
+    case 2128: return launch_bm32<128, 2, 2, 4, DT>(a, gpt, s);
+    case 4032: return launch_bm32<32, 3, 4, 4, DT>(a, gpt, s);
+    case 8064: return launch_bm32<64, 3, 1, 8, DT>(a, gpt, s);
+    case 8128: return launch_bm32<128, 3, 1, 8, DT>(a, gpt, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -418,12 +418,14 @@ def test_gemv_bf16_and_bias(M):
     assert ok, (err, mx)
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032])
+@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_every_tiled_variant(bm, G, dtype, plan):
-    """Each prefill-kernel instantiation (16x16 MFMA row blocks 32/64/128 and
-    32x32 MFMA row blocks 64/128 (codes 1064/1128) x groups per 128-row
+    """Each prefill-kernel instantiation (16x16 MFMA row blocks 32/64/128,
+    32x32 MFMA row blocks 64/128 (codes 1064/1128, 2064/2128 and 4032 with
+    registers for more workgroups per CU, 8064/8128 with 8 waves and 512
+    columns per workgroup) x groups per 128-row
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
     leave the last row block partial; whole pipeline rounds plus a
@@ -448,7 +450,7 @@ def test_every_tiled_variant(bm, G, dtype, plan):
     assert ops.gemm_kernel(20, N, K, G) == "tiled_kernel"
 
 
-@pytest.mark.parametrize("code", [1064, 1128])
+@pytest.mark.parametrize("code", [1064, 1128, 8128])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (14336, 4096)])
 def test_mfma32_kernel_at_llama_prefill_sizes(code, K, N, plan):
     """The 32x32-MFMA prefill kernel at M = 2048 on Llama-3-8B shapes: against the
