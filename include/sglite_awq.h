@@ -166,7 +166,11 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
  *   AWQ_PLAN_SKINNY_VARIANT  decode-kernel shape ntw*10000 + wn*100 + wk
  *   AWQ_PLAN_SKINNY_KS       decode-kernel k-slices
  *   AWQ_PLAN_TILED_MIN_M     smallest M routed to the tiled kernel
- *   AWQ_PLAN_TILED_BM        tiled row block (32, 64 or 128)
+ *   AWQ_PLAN_TILED_BM        tiled row-block code: 32, 64, 128 (16x16x32 MFMA
+ *                            kernel); 1064, 1128, 2064, 2128, 4032 (32x32x16
+ *                            MFMA kernel at 64/128/32 rows with registers for
+ *                            1, 2 or 4 workgroups per CU); 8064, 8128 (its
+ *                            8-wave, 512-column form)
  *   AWQ_PLAN_TILED_KS        tiled k-slices
  *   AWQ_PLAN_KSLICE_VARIANT  k-slice decode-kernel shape wn*100 + wk*10 + kpw
  *                            (M <= 32; any other value leaves the plan alone) */
