@@ -51,6 +51,8 @@ Profiles (summaries committed under profiles/):
       stack70b-4096, mlp)
   rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) ... -- python3 bench.py --pmc-workload;
       python3 bench.py --pmc-summary <fetch_dir> <write_dir>
+  rocprofv3 --marker-trace --kernel-trace -f csv -d <dir> -o bench -- python3 bench.py --profile-workload NAME;
+      python3 bench.py --marker-summary <dir>   (the C ABI's per-call roctx ranges)
 """
 
 from __future__ import annotations
@@ -656,6 +658,41 @@ def profile_workload(name: str, ops, dev: torch.device, gen: torch.Generator) ->
     print(f"profile workload {name} done", flush=True)
 
 
+def marker_summary(trace_dir: str, command: str) -> str:
+    """Markdown summary of a rocprofv3 --marker-trace --kernel-trace run: the roctx ranges the C ABI
+    opens around each compute entry point (host-side span of the call, which encloses its kernel
+    launches), and the kernels dispatched in the same run."""
+    import csv
+    import glob
+
+    def rows(pattern):
+        path = sorted(glob.glob(os.path.join(trace_dir, "**", pattern), recursive=True))[0]
+        with open(path) as f:
+            return list(csv.DictReader(f))
+    ranges: dict = {}
+    for r in rows("*marker_api_trace.csv"):
+        ranges.setdefault(r["Function"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    kernels: dict = {}
+    for r in rows("*kernel_trace.csv"):
+        if "sgl_awq" not in r["Kernel_Name"]:
+            continue  # the workload's own set-up (torch kernels)
+        name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void sgl_awq::", "")
+        kernels.setdefault(name, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = ["# roctx ranges of the C ABI, rocprofv3 marker trace", "",
+           f"Command (from the repository root, TMPDIR=/tmp): `{command}`", "",
+           "Every compute entry point of the C ABI (`awq_repack_cdna4`, `awq_w4a16_gemm[_act|_noalloc]`, the",
+           "MoE stages, the dequantisation probes) opens a roctx range named after itself for the duration",
+           "of the call, so a trace attributes each kernel launch to the operation that issued it.  A range",
+           "spans the host-side call (argument checks, planning, launches); the kernels run asynchronously.",
+           "", "| range | calls | median host us | max host us |", "|---|---|---|---|"]
+    for name, v in sorted(ranges.items()):
+        out.append(f"| `{name}` | {len(v)} | {median(v):.2f} | {max(v):.2f} |")
+    out += ["", "Kernels of the engine in the same run:", "", "| kernel | dispatches | median us |", "|---|---|---|"]
+    for name, v in sorted(kernels.items(), key=lambda kv: -len(kv[1])):
+        out.append(f"| `{name}` | {len(v)} | {median(v):.2f} |")
+    return "\n".join(out) + "\n"
+
+
 def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
     """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
 
@@ -852,14 +889,18 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
             "per_m": per_m}
 
 
-LLAMA_M = (1, 16, 256, 2048, 8192)
+# Config 2's batches, plus the decode batches 64..160 that graph capture
+# covers (multiples of 8 up to the largest decode batch).
+LLAMA_M = (1, 16, 64, 128, 160, 256, 2048, 8192)
 
 
 def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
-    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192), int4 group
-    128, fp16.  M <= 256: graphs of back-to-back launches over `copies` weight copies (1.1 GB);
-    M >= 2048: eager calls.  Median over MEDIAN_SAMPLES samples; GB/s against the HBM peak (and the
-    streaming probe's ceiling at decode sizes) and TFLOP/s against the dense fp16 MFMA peak."""
+    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192) and at the
+    decode batches 64, 128 and 160, int4 group 128, fp16.  M <= 256: graphs of back-to-back launches
+    over `copies` weight copies (1.1 GB); M >= 2048: eager calls.  Median over MEDIAN_SAMPLES
+    samples; GB/s against the HBM peak (and the streaming probe's ceiling at M <= 32) and TFLOP/s
+    against the dense fp16 MFMA peak; `bound` is the roofline the layer's arithmetic intensity
+    (flop per algorithmic byte) puts it under."""
     reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in PREFILL} for _ in range(copies)]
     cnts = {name: ops.make_counters(N, dev) for name, K, N in PREFILL}
     xg = torch.Generator(device=dev).manual_seed(3)
@@ -885,18 +926,18 @@ def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
             info = ops.plan_info(M, N, K, G)
             e = {"us": round(us, 2), "GB/s": round(b / us / 1e3, 1), "TFLOP/s": round(fl / us / 1e6, 1),
                  "kernel": info.kernel, "grid": info.workgroups, "k_slices": info.k_slices}
+            e.update({"frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                      "frac_mfma": round(fl / us / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)})
             if M <= 32:
                 probe = prober.us(b, info.workgroups, info.threads)
-                e.update({"frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4), "ceiling_us": round(probe, 3),
-                          "frac_of_ceiling": round(probe / us, 4)})
-            else:
-                e["frac_mfma"] = round(fl / us / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)
+                e.update({"ceiling_us": round(probe, 3), "frac_of_ceiling": round(probe / us, 4)})
             lin[name] = e
             tb, tf, tt = tb + b, tf + fl, tt + us
         res[str(M)] = {"us_per_layer": round(tt, 2), "GB/s": round(tb / tt / 1e3, 1),
                        "frac_hbm": round(tb / tt / 1e3 / HBM_PEAK_GBS, 4), "TFLOP/s": round(tf / tt / 1e6, 1),
                        "frac_mfma": round(tf / tt / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4),
-                       "bound": "hbm" if M <= 32 else "mfma", "linears": lin}
+                       "bound": "hbm" if tf / tb < MFMA_FP16_PEAK_TFLOPS * 1e3 / HBM_PEAK_GBS else "mfma",
+                       "linears": lin}
         del xs, outs
     del reps
     torch.cuda.synchronize()
@@ -931,7 +972,13 @@ def main() -> int:
                     help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print a markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --pmc-workload")
+    ap.add_argument("--marker-summary", metavar="TRACE_DIR",
+                    help="print a markdown summary of a rocprofv3 --marker-trace --kernel-trace run (the C ABI's "
+                         "roctx ranges) and exit")
     args = ap.parse_args()
+    if args.marker_summary:
+        print(marker_summary(args.marker_summary, args.rocprof_command), end="")
+        return 0
     if args.rocprof_summary:
         section, trace_dir = args.rocprof_summary
         print(rocprof_summary(trace_dir, args.rocprof_command, section), end="")

@@ -7,6 +7,9 @@
  * from device data, so it may be recorded into a HIP graph.  Every function
  * returning int returns 0 on success or a negative AWQ_STATUS_* code; the
  * message of the last failure on the calling thread is awq_last_error().
+ * Each entry point that launches work opens a roctx range named after itself
+ * for the duration of the call (rocprofv3 --marker-trace attributes the
+ * kernels to the operation; the library links librocprofiler-sdk-roctx).
  *
  * Tensor conventions (all row-major, device pointers):
  *   qweight  int32 [K, N/8]   AWQ nibble order [0,2,4,6,1,3,5,7]

@@ -7,6 +7,7 @@
 //   K % G == 0, N % 8 == 0 (layers/quantization/awq.py:76-85)
 // The Python wrapper raises ValueError for AWQ_STATUS_INVALID_ARGUMENT and
 // RuntimeError otherwise.
+#include <rocprofiler-sdk-roctx/roctx.h>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -159,6 +160,18 @@ int scratch_base(hipStream_t stream, char** out) {
   return AWQ_STATUS_OK;
 }
 
+// A roctx range around each compute entry point, named after it: the call
+// shows in a rocprofv3 --marker-trace and encloses the kernels it launches
+// (the per-op ranges the reference's nvtx_annotate gives its layers,
+// utils/torch_utils.py:26-44).  Without a tool attached a push/pop pair is a
+// few tens of nanoseconds.
+struct TraceRange {
+  explicit TraceRange(const char* name) { roctxRangePushA(name); }
+  ~TraceRange() { roctxRangePop(); }
+  TraceRange(const TraceRange&) = delete;
+  TraceRange& operator=(const TraceRange&) = delete;
+};
+
 }  // namespace
 
 extern "C" {
@@ -188,6 +201,7 @@ int64_t awq_repacked_zero_bytes(int64_t K, int64_t N, int64_t G) {
 
 int awq_repack_cdna4(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype, int64_t K,
                      int64_t N, int64_t G, void* w_out, void* s_out, void* z_out, awq_stream_t stream) {
+  const TraceRange range("awq_repack_cdna4");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -202,6 +216,7 @@ int awq_repack_cdna4(const int32_t* qweight, const int32_t* qzeros, const void* 
 
 int awq_unrepack_cdna4(const void* w, const void* s, const void* z, int dtype, int64_t K, int64_t N, int64_t G,
                        int32_t* qweight_out, int32_t* qzeros_out, void* scales_out, awq_stream_t stream) {
+  const TraceRange range("awq_unrepack_cdna4");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -217,6 +232,7 @@ int awq_unrepack_cdna4(const void* w, const void* s, const void* z, int dtype, i
 
 int awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scales, int dtype, int64_t K, int64_t N,
                 int64_t G, void* w_out, awq_stream_t stream) {
+  const TraceRange range("awq_dequant");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -229,6 +245,7 @@ int awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scale
 
 int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype, int64_t K, int64_t N, int64_t G,
                          void* w_out, awq_stream_t stream) {
+  const TraceRange range("awq_dequant_repacked");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -266,6 +283,7 @@ int64_t awq_counter_bytes(int64_t N) {
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                    int64_t M, int64_t N, int64_t K, int64_t G, int dtype, void* ws, int64_t ws_bytes,
                    int32_t* counters, int64_t counter_bytes, awq_stream_t stream) {
+  const TraceRange range("awq_w4a16_gemm");
   Geom g;
   GemmPlan p;
   int st = gemm_prepare(x, w, s, z, bias, out, M, N, K, G, dtype, "awq_w4a16_gemm", &g, &p);
@@ -284,6 +302,7 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
 
 int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                            int64_t M, int64_t N, int64_t K, int64_t G, int dtype, awq_stream_t stream) {
+  const TraceRange range("awq_w4a16_gemm_noalloc");
   Geom g;
   GemmPlan p;
   int st = gemm_prepare(x, w, s, z, bias, out, M, N, K, G, dtype, "awq_w4a16_gemm_noalloc", &g, &p);
@@ -333,6 +352,7 @@ int awq_gemm_kernel_kind_act(int64_t M, int64_t N, int64_t K, int64_t G) {
 int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
                        int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream) {
+  const TraceRange range("awq_w4a16_gemm_act");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -459,6 +479,7 @@ int awq_moe_expert_strides(int64_t K, int64_t N, int64_t G, int64_t* w_stride, i
 
 int awq_moe_topk_softmax(const float* gating_output, float* topk_weights, int32_t* topk_ids, int64_t T, int64_t E,
                          int64_t topk, int renormalize, awq_stream_t stream) {
+  const TraceRange range("awq_moe_topk_softmax");
   if (T < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_topk_softmax: T must be non-negative");
   if (E <= 0 || E > 512) return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_topk_softmax: E must be in [1, 512], got %lld",
                                      (long long)E);
@@ -477,6 +498,7 @@ int awq_moe_topk_softmax(const float* gating_output, float* topk_weights, int32_
 int awq_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_size,
                              int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
                              int32_t* expert_offsets, awq_stream_t stream) {
+  const TraceRange range("awq_moe_align_block_size");
   if (E <= 0 || E > 512)
     return fail(AWQ_STATUS_UNSUPPORTED, "awq_moe_align_block_size: E must be in [1, 512], got %lld", (long long)E);
   if (block_size <= 0 || block_size % 16 != 0 || block_size > 1024)
@@ -497,6 +519,7 @@ int awq_moe_w4a16_gemm(const void* a, int64_t a_rows, const void* w, const void*
                        int64_t N, int64_t K, int64_t G, int dtype, const int32_t* sorted_ids, int64_t sorted_cap,
                        const int32_t* expert_offsets, const float* topk_weights, int64_t num_routed, int64_t top_k,
                        int activation, int mul_routed_weight, void* out, awq_stream_t stream) {
+  const TraceRange range("awq_moe_w4a16_gemm");
   int64_t Gr = 0;
   int st = check_shape(K, N, G, dtype, &Gr);
   if (st != 0) return st;
@@ -545,6 +568,7 @@ int awq_moe_w4a16_gemm(const void* a, int64_t a_rows, const void* w, const void*
 
 int awq_moe_sum_reduce(const void* in, void* out, int64_t T, int64_t topk, int64_t H, int dtype,
                        awq_stream_t stream) {
+  const TraceRange range("awq_moe_sum_reduce");
   if (dtype != AWQ_DTYPE_FP16 && dtype != AWQ_DTYPE_BF16)
     return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_moe_sum_reduce: dtype must be 0 or 1, got %d", dtype);
   if (T < 0 || topk <= 0 || H <= 0 || H % 8 != 0)
