@@ -346,6 +346,12 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 2064, 2128 = the same with registers for two workgroups per CU;
     // 4032 = the same at 32 rows with registers for four;
     // 8064, 8128 = 8 waves and 512 columns per workgroup, one per CU.
+    // 32-row blocks beyond 32 rows, up to 160, on layers of at most 8192
+    // columns and 8192 rows of K (graph-replay A/B at M = 48..160 over the
+    // Llama-3-8B and Qwen3-4B linears: qkv and o 7-19% faster in the 32x32
+    // kernel with four workgroups per CU; wider or deeper layers, gate_up and
+    // down, 3-16% slower, so they keep 64- and 128-row blocks).
+    const bool bm32_ok = g.M <= 32 || (g.M <= 160 && g.N <= 8192 && g.K <= 8192);
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
                            env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128;
@@ -356,7 +362,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128}) {
       const int bm = code % 1000;
       if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
-      if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && g.M > 32)) continue;
+      if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && !bm32_ok)) continue;
       const int64_t tiles = ((g.NT + 15) / 16) * ((g.M + bm - 1) / bm);
       const int64_t min_ktc = g.M <= 32 ? 2 : 4;  // k-tiles per slice at least
       for (int ks : {1, 2, 3, 4, 6, 8, 12, 16}) {
