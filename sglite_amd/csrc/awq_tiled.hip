@@ -78,6 +78,56 @@ __device__ __forceinline__ void tile_of(int b, int gx, int gy, int& bx, int& by)
   by = grp * 4 + r % rows;
 }
 
+// Zero points and scales of a workgroup's TPW = 4 NW column tiles, staged in
+// LDS in chunks of 6 quantisation groups: zero words [tile][group][8 B] in
+// the first TPW / 16 KiB, scales [tile][group][16 x 2 B] in the rest, one
+// 1 KiB buffer load into LDS per wave and chunk (waves below kZD copy zero
+// words -- 16-byte slot i of the region is tile i / 3, groups 2 (i % 3) and
+// + 1, slots past 3 TPW repeat slot 0 -- the others scales: slot i is tile
+// i / 12, bytes 16 (i % 12) of its 192).  Tile slots are the workgroup's
+// tiles in order, or with a fused gate/up activation its TPW / 2 gate tiles
+// then their up tiles.  A chunk's first group goes in the scalar offset;
+// groups past a tile's last read the next tile's (or, past the array,
+// zeros) and are never used.
+template <int NW>
+struct ZsChunks {
+  static constexpr int TPW = 4 * NW;
+  static constexpr int kZD = TPW / 16;  // zero-word loads per chunk
+  static constexpr int kSlots = NW * 64;  // 16-byte slots per chunk buffer
+  static_assert(kZD * 64 >= 3 * TPW && (NW - kZD) * 64 == 12 * TPW, "one load per wave");
+  __amdgpu_buffer_rsrc_t src;
+  uint32_t off;
+  bool zero;
+  __device__ void init(const TiledArgs& a, int bx, int wave, int lane) {
+    zero = wave < kZD;
+    src = zero ? make_rsrc(a.z, (uint32_t)a.NT * (uint32_t)a.NG * 8u)
+               : make_rsrc(a.s, (uint32_t)a.NT * (uint32_t)a.NG * 32u);
+    auto slot_tile = [&](int u) {
+      const int NTg = a.NT >> 1;
+      const int tt = a.act ? (u < TPW / 2 ? bx * (TPW / 2) + u : NTg + bx * (TPW / 2) + u - TPW / 2) : bx * TPW + u;
+      return (uint32_t)min(tt, a.NT - 1);
+    };
+    int si = wave * 64 + lane;
+    if (zero) {
+      si = si < 3 * TPW ? si : 0;
+      off = slot_tile(si / 3) * (uint32_t)a.NG * 8u + (uint32_t)(si % 3) * 16u;
+    } else {
+      si -= kZD * 64;
+      off = slot_tile(si / 12) * (uint32_t)a.NG * 32u + (uint32_t)(si % 12) * 16u;
+    }
+  }
+  // The chunk starting at group g0 into buf.
+  __device__ void copy(u32x4* buf, int g0, int wave) const {
+    load_lds16(src, &buf[wave * 64], off, zero ? g0 * 8 : g0 * 32);
+  }
+  // Byte offsets in a chunk of the zero word and the scale of column c of
+  // tile slot u, group 0 of the chunk (group i: + 8 i, + 32 i).
+  static __device__ uint32_t zero_at(int u, int c) { return (uint32_t)u * 48u + (uint32_t)(c >> 3) * 4u; }
+  static __device__ uint32_t scale_at(int u, int c) {
+    return (uint32_t)kZD * 1024u + (uint32_t)u * 192u + (uint32_t)c * 2u;
+  }
+};
+
 template <int GPT>
 struct WStage {
   u32x4 q[4];          // one 16-byte weight vector per column tile
@@ -93,7 +143,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   constexpr int MTL = BM / 16;
   constexpr int NTW = 4;
   constexpr int XS = MTL * 4 * 64;              // 16-byte slots per activation buffer
-  constexpr int kLoadsW = NTW * (1 + 2 * GPT);  // load instructions per weight stage
+  // Zero points and scales: with at most 6 groups per NS k-tiles they reach
+  // LDS in ZsChunks, one chunk per NS k-tiles, double-buffered; otherwise each
+  // stage loads them (2 GPT loads per tile).
+  constexpr bool kZsLds = NS * GPT <= 6;
+  using ZC = ZsChunks<4>;
+  constexpr int kLoadsW = kZsLds ? NTW : NTW * (1 + 2 * GPT);  // load instructions per weight stage
   // Loads issued after a k-tile's activations, up to the end of the step
   // before that k-tile: its own weights and the NS - 2 k-tiles behind it.
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * MTL;
@@ -106,6 +161,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   __shared__ u32x4 xs2[NS > 2 ? XS : 1];
   __shared__ u32x4 xs3[NS > 3 ? XS : 1];
   __shared__ u32x4 xs4[NS > 4 ? XS : 1];
+  __shared__ u32x4 zsl[kZsLds ? 2 : 1][kZsLds ? ZC::kSlots : 1];  // zero-point / scale chunks
   auto xbuf = [&](int p) -> u32x4* {
     return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : (p == 3 ? xs3 : xs4)));
   };
@@ -160,17 +216,31 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     const int base = min(q == 0 ? pb0 : pb1, a.NT - 1);
     const uint32_t ntiles = (uint32_t)min(2, a.NT - base);
     wr[q] = make_rsrc(a.w + (int64_t)base * KT * 64, ntiles * (uint32_t)KT * 1024u);
-    zr[q] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
-    sr[q] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
+    if constexpr (!kZsLds) {
+      zr[q] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
+      sr[q] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int j = 2 * q + h;
       const uint32_t dt = (uint32_t)(min(pt[j], a.NT - 1) - base);
       woff[j] = dt * (uint32_t)KT * 1024u + (uint32_t)lane * 16u;
-      zoff[j] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
-      soff[j] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+      if constexpr (kZsLds) {
+        // Slot j's tile slot in a chunk, and its zero word's and scale's offsets.
+        const int u = a.act ? (q == 0 ? 0 : ZC::TPW / 2) + wave * 2 + h : wave * NTW + j;
+        zoff[j] = ZC::zero_at(u, c);
+        soff[j] = ZC::scale_at(u, c);
+      } else {
+        zoff[j] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
+        soff[j] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+      }
     }
   }
+  ZC zc;
+  if constexpr (kZsLds) zc.init(a, bx, wave, lane);
+  // Chunk ci: k-tiles kt0 + ci NS .. + NS - 1.
+  auto chunk_g0 = [&](int ci) { return ((kt0 + ci * NS) * 128) >> a.gshift; };
+  auto dma_chunk = [&](int ci) { zc.copy(zsl[ci & 1], chunk_g0(ci), wave); };
   // Zero-length range for the prefetches past the k-slice: the loads are
   // still issued (every wait count assumes a fixed number of loads per
   // step) but return zeros without a memory access.
@@ -199,15 +269,33 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     const int g0 = (kt * 128) >> a.gshift;  // first group of the k-tile
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      const __amdgpu_buffer_rsrc_t rw = live ? wr[j >> 1] : r0, rz = live ? zr[j >> 1] : r0,
-                                   rs = live ? sr[j >> 1] : r0;
+      const __amdgpu_buffer_rsrc_t rw = live ? wr[j >> 1] : r0;
       S.q[j] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[j], kt * 1024, 0);
+      if constexpr (!kZsLds) {
+        const __amdgpu_buffer_rsrc_t rz = live ? zr[j >> 1] : r0, rs = live ? sr[j >> 1] : r0;
 #pragma unroll
-      for (int g = 0; g < GPT; ++g) S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[j] + 8 * g, g0 * 8, 0);
+        for (int g = 0; g < GPT; ++g)
+          S.z[j][g] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[j] + 8 * g, g0 * 8, 0);
 #pragma unroll
-      for (int g = 0; g < GPT; ++g)
-        S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[j] + 32 * g, g0 * 32, 0);
+        for (int g = 0; g < GPT; ++g)
+          S.s[j][g] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[j] + 32 * g, g0 * 32, 0);
+      }
     }
+  };
+  // Zero words and scales of k-tile kt from its chunk (k-tiles past the
+  // slice are never computed: they read the last live one's).
+  auto read_zs = [&](WStage<GPT>& S, int kt) {
+    kt = min(kt, kend - 1);
+    const int ci = (kt - kt0) / NS;
+    const int gi = ((kt * 128) >> a.gshift) - chunk_g0(ci);
+    const char* buf = (const char*)zsl[ci & 1];
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+      for (int g = 0; g < GPT; ++g) {
+        S.z[j][g] = *(const uint32_t*)(buf + zoff[j] + (uint32_t)(gi + g) * 8u);
+        S.s[j][g] = *(const uint16_t*)(buf + soff[j] + (uint32_t)(gi + g) * 32u);
+      }
   };
 
   WStage<GPT> st[NS];
@@ -258,9 +346,18 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // stage pa (activations during blocks 0 and 1, weights during block 2), and
   // block 3 already prepares block 0 of k-tile kt + 1 (stage pn), so no step
   // starts with dequantisation work that no MFMA overlaps.
+  // Zero-point / scale chunk ci + 2 is copied at the start of the second step
+  // of the loop iteration that computes chunk ci's k-tiles: after the barrier
+  // that ends chunk ci's last read (the first step's weight issue), and ahead
+  // of the activation loads that the wait before its own first read (the
+  // next iteration's second step) covers.
   auto step = [&](int p, int kt) {
     const int pa = (p + NS - 1) % NS, pn = (p + 1) % NS;
     const int ka = kt + NS - 1;
+    if constexpr (kZsLds) {
+      if (p == 1) dma_chunk((kt - 1 - kt0) / NS + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     load_x(pa, ka, 0, MTL / 2);
     __builtin_amdgcn_sched_barrier(0);
     fetch(1, st[p], xbuf(p), 1);
@@ -271,6 +368,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     mma(1);
     load_w(st[pa], ka);  // the wait counts rely on this issue order
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kZsLds) {
+      // Issued before the next LDS reads, whose waits then cover them before
+      // the barrier after which a chunk buffer may be refilled.
+      read_zs(st[pa], ka);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     fetch(1, st[p], xbuf(p), 3);
     mma(0);
     sync_step();
@@ -279,7 +382,13 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     mma(1);
   };
 
-  // Prologue: k-tiles 0 .. NS - 2 in flight, block 0 of k-tile 0 prepared.
+  // Prologue: zero-point / scale chunks 0 and 1, k-tiles 0 .. NS - 2 in
+  // flight, block 0 of k-tile 0 prepared.
+  if constexpr (kZsLds) {
+    dma_chunk(0);
+    dma_chunk(1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p) {
     load_x(p, kt0 + p, 0, MTL);
@@ -288,6 +397,10 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
   sync_step();
+  if constexpr (kZsLds) {
+#pragma unroll
+    for (int p = 0; p + 1 < NS; ++p) read_zs(st[p], kt0 + p);
+  }
   make_zs(st[0]);
   fetch(0, st[0], xbuf(0), 0);
 
@@ -443,13 +556,19 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   constexpr int XF = MT * 8;               // activation fragments (1 KiB) per k-tile
   static_assert(XF % NW == 0, "whole activation fragments per wave");
   constexpr int XPW = XF / NW;             // ... loaded by each wave
-  constexpr int kLoadsW = 4 + 4 * GPT;     // weight-stage load instructions per k-tile
+  // Zero points and scales: with at most 6 groups per NS k-tiles they reach
+  // LDS in ZsChunks, one chunk per NS k-tiles, double-buffered; otherwise each
+  // stage loads them (4 GPT loads per wave).
+  constexpr bool kZsLds = NS * GPT <= 6;
+  using ZC = ZsChunks<NW>;
+  constexpr int kLoadsW = kZsLds ? 4 : 4 + 4 * GPT;  // weight-stage load instructions per k-tile
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
   static_assert(kAfterX < 64, "vector-memory counter range");
   __shared__ u32x4 xs0[XF * 64];
   __shared__ u32x4 xs1[XF * 64];
   __shared__ u32x4 xs2[NS > 2 ? XF * 64 : 1];
   __shared__ u32x4 xs3[NS > 3 ? XF * 64 : 1];
+  __shared__ u32x4 zsl[kZsLds ? 2 : 1][kZsLds ? ZC::kSlots : 1];  // zero-point / scale chunks
   auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : xs3)); };
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -499,15 +618,27 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     const int base = min(g == 0 ? pb0 : pb1, a.NT - 1);
     const uint32_t ntiles = (uint32_t)min(2, a.NT - base);
     wr[g] = make_rsrc(a.w + (int64_t)base * KT * 64, ntiles * (uint32_t)KT * 1024u);
-    zr[g] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
-    sr[g] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
     const uint32_t dt = (uint32_t)(min(pt[2 * g + t], a.NT - 1) - base);  // this lane's tile in the range
     woff[g] = dt * (uint32_t)KT * 1024u + (uint32_t)(c + 16 * h) * 16u;  // + 512 for the odd-step vector
-    zoff[g] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
-    soff[g] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+    if constexpr (kZsLds) {
+      // This lane's tile slot in a chunk, and its zero word's and scale's offsets.
+      const int u = a.act ? (g == 0 ? 0 : ZC::TPW / 2) + wave * 2 + t : wave * 4 + 2 * g + t;
+      zoff[g] = ZC::zero_at(u, c);
+      soff[g] = ZC::scale_at(u, c);
+    } else {
+      zr[g] = make_rsrc(a.z + (int64_t)base * NG, ntiles * (uint32_t)NG * 8u);
+      sr[g] = make_rsrc(a.s + (int64_t)base * NG * 16, ntiles * (uint32_t)NG * 32u);
+      zoff[g] = dt * (uint32_t)NG * 8u + (uint32_t)(c >> 3) * 4u;
+      soff[g] = (dt * (uint32_t)NG * 16u + (uint32_t)c) * 2u;
+    }
   }
   const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.w, 0u);
   const uint32_t zshift = 4u * (uint32_t)(c & 7);
+  ZC zc;
+  if constexpr (kZsLds) zc.init(a, bx, wave, lane);
+  // Chunk ci: k-tiles kt0 + ci NS .. + NS - 1.
+  auto chunk_g0 = [&](int ci) { return ((kt0 + ci * NS) * 128) >> a.gshift; };
+  auto dma_chunk = [&](int ci) { zc.copy(zsl[ci & 1], chunk_g0(ci), wave); };
 
   f32x16 acc[MT][2];
 #pragma unroll
@@ -533,15 +664,34 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     const int g0 = (kt * 128) >> a.gshift;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const __amdgpu_buffer_rsrc_t rw = live ? wr[g] : r0, rz = live ? zr[g] : r0, rs = live ? sr[g] : r0;
+      const __amdgpu_buffer_rsrc_t rw = live ? wr[g] : r0;
       S.q[g][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g], kt * 1024, 0);
       S.q[g][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g] + 512u, kt * 1024, 0);
+      if constexpr (!kZsLds) {
+        const __amdgpu_buffer_rsrc_t rz = live ? zr[g] : r0, rs = live ? sr[g] : r0;
 #pragma unroll
-      for (int q = 0; q < GPT; ++q) S.z[g][q] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[g] + 8 * q, g0 * 8, 0);
+        for (int q = 0; q < GPT; ++q)
+          S.z[g][q] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[g] + 8 * q, g0 * 8, 0);
 #pragma unroll
-      for (int q = 0; q < GPT; ++q)
-        S.s[g][q] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[g] + 32 * q, g0 * 32, 0);
+        for (int q = 0; q < GPT; ++q)
+          S.s[g][q] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[g] + 32 * q, g0 * 32, 0);
+      }
     }
+  };
+  // Zero words and scales of k-tile kt from its chunk (k-tiles past the
+  // slice are never computed: they read the last live one's).
+  auto read_zs = [&](WStage32<GPT>& S, int kt) {
+    kt = min(kt, kend - 1);
+    const int ci = (kt - kt0) / NS;
+    const int gi = ((kt * 128) >> a.gshift) - chunk_g0(ci);
+    const char* buf = (const char*)zsl[ci & 1];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int q = 0; q < GPT; ++q) {
+        S.z[g][q] = *(const uint32_t*)(buf + zoff[g] + (uint32_t)(gi + q) * 8u);
+        S.s[g][q] = *(const uint16_t*)(buf + soff[g] + (uint32_t)(gi + q) * 32u);
+      }
   };
   // One k-tile: 8 k-steps of MT x 2 MFMAs.  The LDS reads and the
   // dequantisation of step s + 1 are issued between step s's MFMAs (one LDS
@@ -593,7 +743,18 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     asm volatile("" ::: "memory");
   };
 
+  // Issue order (the wait counts rely on it): chunk DMAs, activations, weights.
+  // Chunks 0 and 1 are copied first; chunk ci + 2 in the second step of the
+  // loop iteration that computes chunk ci's k-tiles, after the barrier that
+  // ends chunk ci's last read (the first step's issue of k-tile
+  // kt0 + ci NS + NS - 1), and more than one wait ahead of its first read
+  // (the second step of the next iteration).
   WStage32<GPT> stg[NS];
+  if constexpr (kZsLds) {
+    dma_chunk(0);
+    dma_chunk(1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p) {
     load_x(p, kt0 + p);
@@ -602,12 +763,26 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
   sync_step();
+  if constexpr (kZsLds) {
+#pragma unroll
+    for (int p = 0; p + 1 < NS; ++p) read_zs(stg[p], kt0 + p);
+  }
   auto step = [&](int p, int kt) {
     const int pa = (p + NS - 1) % NS;
+    if constexpr (kZsLds) {
+      if (p == 1) dma_chunk((kt - 1 - kt0) / NS + 2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     load_x(pa, kt + NS - 1);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(stg[pa], kt + NS - 1);  // the wait counts rely on this issue order
+    load_w(stg[pa], kt + NS - 1);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kZsLds) {
+      // Issued before the compute's LDS reads, whose waits then cover them
+      // before the barrier after which a chunk buffer may be refilled.
+      read_zs(stg[pa], kt + NS - 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     compute(stg[p], xbuf(p));
     sync_step();
   };
