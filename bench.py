@@ -37,6 +37,8 @@ Also reported on the same line:
   moe           config 4: the Qwen3-30B-A3B-shaped grouped MoE forward.
   stack70b      config 3: the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at
                 M = 64 (GB/s, one graph per pass) and M = 4096 (TFLOP/s).
+  bounds        the MFMA-rate probe (awq_mfma_probe) at one and two waves per
+                SIMD: the compute bound the prefill TFLOP/s are read against.
   cpu_baseline  the CPU oracle on the host cores for configs 0-4 (dequantisation
                 and matmul timed separately, 2 warm-ups, median of 5); value is
                 config 1 in GB/s.
@@ -48,7 +50,7 @@ Profiles (summaries committed under profiles/):
       --no-cpu-baseline --no-prefill --no-moe --no-stack --no-mlp;  python3 bench.py --rocprof-summary decode <dir>
   rocprofv3 --kernel-trace --stats -f csv -d <dir> -o bench -- python3 bench.py --profile-workload NAME;
       python3 bench.py --rocprof-summary NAME <dir>   (NAME: prefill-2048, prefill-8192, moe, stack70b-64,
-      stack70b-4096, mlp)
+      stack70b-4096, mlp, probes)
   rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) ... -- python3 bench.py --pmc-workload;
       python3 bench.py --pmc-summary <fetch_dir> <write_dir>
   rocprofv3 --marker-trace --kernel-trace -f csv -d <dir> -o bench -- python3 bench.py --profile-workload NAME;
@@ -626,6 +628,42 @@ def _trace_table(groups) -> list:
 
 PROFILE_REPS = 10  # timed calls per shape in the --profile-workload runs (after 2 warm-ups)
 
+PROBE_ITERS = 4000  # rounds of eight 32x32x16 MFMAs per wave in one MFMA-probe launch
+PROBE_FLOP_PER_WAVE_ITER = 8 * 2 * 32 * 32 * 16
+
+
+def probe_grids(ops) -> dict:
+    """MFMA-probe grids: 256-thread workgroups, one and two per CU (one and two waves per SIMD)."""
+    cus = ops.device_cu_count()
+    return {"1_wave_per_simd": cus, "2_waves_per_simd": 2 * cus}
+
+
+def bounds_bench(ops, dev: torch.device, reps: int = 7) -> dict:
+    """Compute bounds the prefill kernels are read against: the MFMA probe (awq_mfma_probe: eight
+    independent 32x32x16 fp16 MFMAs per wave, operands in registers, no memory traffic) at one and
+    two waves per SIMD, median of `reps` launches each; TFLOP/s and fraction of the 2.5 PFLOP/s
+    dense peak.  A W4A16 GEMM also spends vector-ALU time dequantising every weight between its MFMAs,
+    so its attainable rate lies below the probe's."""
+    sink = torch.empty(4 * 2 * ops.device_cu_count(), dtype=torch.float32, device=dev)
+    out = {"probe": "awq_mfma_probe, eight independent v_mfma_f32_32x32x16_f16 per wave, "
+                    f"{PROBE_ITERS} rounds per launch, 256-thread workgroups"}
+    for label, grid in probe_grids(ops).items():
+        ops.mfma_probe(PROBE_ITERS, grid, 256, sink)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            ops.mfma_probe(PROBE_ITERS, grid, 256, sink)
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e-3)
+        t = median(ts)
+        tf = grid * 4 * PROBE_ITERS * PROBE_FLOP_PER_WAVE_ITER / t / 1e12
+        out[label] = {"workgroups": grid, "us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+                      "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+    return out
+
 
 def _launches_per_call(ops, M: int, N: int, K: int, activation=None) -> int:
     info = ops.plan_info(M, N, K, G, activation)
@@ -652,6 +690,12 @@ def profile_workload(name: str, ops, dev: torch.device, gen: torch.Generator) ->
         stack70b_bench(ops, dev, gen, only_m=int(name.split("-")[1]))
     elif name == "mlp":
         mlp_bench(ops, dev, gen, reps=20)
+    elif name == "probes":
+        sink = torch.empty(4 * 2 * ops.device_cu_count(), dtype=torch.float32, device=dev)
+        for grid in probe_grids(ops).values():
+            for _ in range(2 + PROFILE_REPS):
+                ops.mfma_probe(PROBE_ITERS, grid, 256, sink)
+            torch.cuda.synchronize()
     else:
         raise ValueError(f"unknown profile workload {name!r}")
     torch.cuda.synchronize()
@@ -693,6 +737,40 @@ def marker_summary(trace_dir: str, command: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def _probe_summary(trace_dir: str, command: str, ops) -> str:
+    import csv
+    import glob
+
+    path = sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True))[0]
+    runs: dict = {}
+    for r in csv.DictReader(open(path)):
+        if "mfma_probe_kernel" not in r["Kernel_Name"]:
+            continue
+        wgs = int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"])
+        runs.setdefault(wgs, []).append((int(r["Start_Timestamp"]),
+                                         (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3))
+    runs = {wgs: [d for _, d in sorted(v)] for wgs, v in runs.items()}  # launch order
+    lines = ["# MFMA-rate probe (the compute bound of the prefill kernels), rocprofv3 kernel trace", "",
+             f"Command (from the repository root, TMPDIR=/tmp): `{command}`", "",
+             "`mfma_probe_kernel`: eight independent `v_mfma_f32_32x32x16_f16` per wave, operands in registers,",
+             f"no memory traffic, {PROBE_ITERS} rounds per launch, 256-thread workgroups; one workgroup per CU is one",
+             "wave per SIMD, two are two.  Per grid 2 warm-ups then the timed launches, back to back (mean of",
+             "those; the first and last timed launch show any clock change under the sustained load).  The",
+             "benchmark's `bounds` section times isolated launches (a synchronisation between them) instead.",
+             "The prefill kernels dequantise every weight on the vector ALU between their MFMAs, so they are",
+             "read against this rate, not against the 2.5 PFLOP/s peak alone.", "",
+             "| workgroups | waves per SIMD | launches | mean us | first us | last us | TFLOP/s | fraction of 2.5 PFLOP/s |",
+             "|---|---|---|---|---|---|---|---|"]
+    cus = ops.device_cu_count()
+    for wgs, ds in sorted(runs.items()):
+        timed = ds[2:] if len(ds) > 2 else ds
+        us = sum(timed) / len(timed)
+        tf = wgs * 4 * PROBE_ITERS * PROBE_FLOP_PER_WAVE_ITER / (us * 1e-6) / 1e12
+        lines.append(f"| {wgs} | {wgs // cus} | {len(timed)} | {us:.1f} | {timed[0]:.1f} | {timed[-1]:.1f} | {tf:.1f} | "
+                     f"{tf / MFMA_FP16_PEAK_TFLOPS:.4f} |")
+    return "\n".join(lines) + "\n"
+
+
 def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
     """Markdown summary of a rocprofv3 --kernel-trace run of this benchmark.
 
@@ -704,8 +782,12 @@ def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
     each launched 2 + PROFILE_REPS times in order; per linear the mean of the
     timed calls (GEMM plus any reduction) and TFLOP/s.
     moe, stack70b-M, mlp: the section's kernels with their durations.
+    probes: the MFMA probe at one and two waves per SIMD (mean of the timed launches).
     """
     from sglite_amd import ops
+
+    if section == "probes":
+        return _probe_summary(trace_dir, command, ops)
 
     groups = _trace_groups(trace_dir)
     head = [f"Command (from the repository root, TMPDIR=/tmp): `{command}`", ""]
@@ -967,7 +1049,7 @@ def main() -> int:
                     help="the profiled command, quoted in the summary's header")
     ap.add_argument("--profile-workload", metavar="NAME",
                     help="run one section's launch sequence for rocprofv3 --kernel-trace and exit: prefill-2048, "
-                         "prefill-8192, moe, stack70b-64, stack70b-4096 or mlp")
+                         "prefill-8192, moe, stack70b-64, stack70b-4096, mlp or probes")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -1061,6 +1143,11 @@ def main() -> int:
         progress("70b stack")
         stack = stack70b_bench(ops, dev, gen)
 
+    bounds = None
+    if not args.no_prefill:
+        progress("mfma probe")
+        bounds = bounds_bench(ops, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         progress("cpu baseline")
@@ -1096,6 +1183,7 @@ def main() -> int:
         "mlp": mlp,
         "moe": moe,
         "stack70b": stack,
+        "bounds": bounds,
     }
     print(json.dumps(line))
     return 0
