@@ -220,8 +220,10 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
 //    kernel);
 //  * 10-16 rows: K >= 8192 and K * N >= 40M (14336 x 4096 down: 19.4 ->
 //    15.4 us at M = 16; 28672 x 8192 down: 67.7 -> 37.3 us);
-//  * 6-9 rows: K >= 8192 and 8192 <= N < 32768 (the 70B qkv, o and down
-//    projections: 48.7 -> 36.4 us for the down projection at M = 8);
+//  * 6-9 rows: K >= 8192 and 4096 <= N < 32768 (the 70B qkv, o and down
+//    projections: 48.7 -> 36.4 us for the down projection at M = 8; the
+//    Llama-3-8B down, 14336 x 4096: 16.5 -> 13.8 us at M = 8 on the 32-row
+//    32x32 kernel with 16 k-slices);
 //  * 14-16 rows on gate_up-sized matrices (N >= 16384, K * N >= 20M).
 // A fused gate/up activation uses the 17-32 and 14-16 row rules only.
 bool tiled_preferred(const Geom& g, int act) {
@@ -233,7 +235,7 @@ bool tiled_preferred(const Geom& g, int act) {
   if (g.M >= 14 && g.N >= 16384 && kn >= 20000000) return true;
   if (act) return false;
   if (g.M >= 10) return g.K >= 8192 && kn >= 40000000;
-  return g.M >= 6 && g.K >= 8192 && g.N >= 8192 && g.N < 32768;
+  return g.M >= 6 && g.K >= 8192 && g.N >= 4096 && g.N < 32768;
 }
 
 // k-slice kernel plan of shape v (wn * 100 + wk * 10 + kpw): one k-slice of
@@ -388,12 +390,13 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // (Llama-3-8B gate_up at M = 2048: 472 -> 432 us; every linear at
     // M = 8192: 3-8% faster).  On one wave of tiles the second workgroup has
     // nothing to overlap with and the 16x16 kernel's deeper prefetch wins.
-    // Batches of up to 32 rows split in at most 8 k-slices, one group per
-    // k-tile: the 32x32-MFMA kernel at 32 rows with registers for four
-    // workgroups per CU (graph-replay sweep of the Qwen3-4B and Llama-3-8B
-    // linears at M = 16 and 32: 4-12% faster, e.g. Qwen3-4B gate_up at M = 16
-    // 15.1 -> 13.3 us; with 16 slices its longer reduction chains lose).
-    if (!env_bm_ok && best_bm == 32 && ks <= 8 && g.G >= 128) best_bm = 4032;
+    // 32-row blocks with one group per k-tile: the 32x32-MFMA kernel at 32
+    // rows with registers for four workgroups per CU (graph-replay sweep of
+    // the Qwen3-4B and Llama-3-8B linears at M = 16 and 32: 4-12% faster, e.g.
+    // Qwen3-4B gate_up at M = 16 15.1 -> 13.3 us; since its zero points and
+    // scales come from LDS also at 12-16 k-slices: Llama-3-8B down at M = 12,
+    // 16, 32 15.6 -> 14.1, 15.7 -> 14.6, 17.2 -> 16.9 us).
+    if (!env_bm_ok && best_bm == 32 && g.G >= 128) best_bm = 4032;
     if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64 &&
         ((g.NT + 15) / 16) * ((g.M + 127) / 128) * 2 >= 3 * (int64_t)g.cus)
       best_bm = 2128;

@@ -85,7 +85,7 @@ def test_workspace_query_is_bounded():
     (9728, 2560, "g" * 7 + "k" * 9),           # Qwen3-4B down: 76 k-tiles, k-slice kernel from 8 rows
     (4096, 6144, "g" * 16),                    # Llama-3-8B qkv
     (4096, 28672, "g" * 4 + "s" * 9 + "t" * 3),  # Llama-3-8B gate_up: wide
-    (14336, 4096, "g" * 9 + "t" * 7),          # Llama-3-8B down: deep
+    (14336, 4096, "g" * 5 + "t" * 11),         # Llama-3-8B down: deep, 32-row 32x32 kernel from 6 rows
     (8192, 10240, "g" * 5 + "t" * 11),         # Llama-3-70B qkv
     (8192, 57344, "gg" + "s" * 7 + "t" * 7),   # Llama-3-70B gate_up: very wide
     (28672, 8192, "g" * 5 + "t" * 11),         # Llama-3-70B down
