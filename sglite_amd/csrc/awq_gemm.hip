@@ -411,6 +411,20 @@ GemmPlan plan_gemm(const Geom& g, int act) {
       const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 127) / 128);
       if (t8 <= g.cus || t8 % g.cus == 0) best_bm = 8128;
     }
+    // Batches of up to 256 rows with K unsplit, one group per k-tile
+    // (graph-replay sweep of the Qwen3-4B and Llama-3-8B linears at M =
+    // 96..256): a 128-row block on a grid whose 64 x 512 tiles fill at most
+    // three quarters of the CUs takes the 8-wave 64-row form (two waves per
+    // SIMD, less row padding: Llama-3-8B gate_up at M = 160 / 192 69.8 ->
+    // 61.5 / 71.1 -> 63.3 us, Qwen3-4B gate_up at M = 224 44.1 -> 39.6 us;
+    // on fuller grids it was 0.5-3% slower), and a 64-row block the two-
+    // workgroup 32x32 form (Qwen3-4B gate_up at M = 128 30.5 -> 28.2 us, 1-8%
+    // faster in every case measured).
+    if (!env_bm_ok && ks == 1 && g.G >= 128 && g.M <= 256) {
+      const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 63) / 64);
+      if (best_bm == 128 && 4 * t8 <= 3 * (int64_t)g.cus) best_bm = 8064;
+      else if (best_bm == 64) best_bm = 2064;
+    }
     p.variant = best_bm;
     p.grid_x = best_bm >= 8000 ? (g.NT + 31) / 32 : (g.NT + 15) / 16;
     p.grid_y = (g.M + best_bm % 1000 - 1) / (best_bm % 1000);
