@@ -233,6 +233,27 @@ def test_plan_overrides_and_plan_info():
     assert ops.device_cu_count() >= 1
 
 
+@pytest.mark.parametrize("M,N,K,variant,ks,wgs", [
+    (8, 4096, 14336, 4032, 16, 256),     # Llama-3-8B down: 32-row 32x32 form, 16 k-slices
+    (32, 4096, 14336, 4032, 16, 256),
+    (128, 28672, 4096, 2064, 1, 224),    # Llama-3-8B gate_up: two-workgroup 64-row 32x32 form
+    (160, 28672, 4096, 8064, 1, 168),    # 8-wave 64-row form: 168 of 256 CUs
+    (256, 19456, 2560, 8064, 1, 152),    # Qwen3-4B gate_up
+    (224, 28672, 4096, 128, 1, 224),     # 64 x 512 tiles would fill 224 CUs: 16x16 128-row block
+    (2048, 28672, 4096, 2128, 1, 1792),  # 3.5 rounds: two workgroups per CU
+    (2048, 6144, 4096, 8128, 1, 192),    # at most one round of 512-column tiles
+    (2048, 4096, 4096, 128, 1, 256),     # one round of 256-column tiles
+    (8192, 28672, 4096, 8128, 1, 3584),  # whole rounds
+])
+def test_tiled_plan_forms(M, N, K, variant, ks, wgs):
+    """The planner's row-block form per batch size on a whole MI355X (256 CUs, the
+    host-side planning default)."""
+    if ops.device_cu_count() != 256:
+        pytest.skip("the forms are pinned for a whole MI355X (256 CUs)")
+    info = ops.plan_info(M, N, K, 128)
+    assert (info.kernel, info.variant, info.k_slices, info.workgroups) == ("tiled_kernel", variant, ks, wgs)
+
+
 def test_stream_probe_validates_before_launch():
     lib = _lib.load()
     fake = 0x10000
