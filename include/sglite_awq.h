@@ -85,9 +85,9 @@ int awq_dequant(const int32_t* qweight, const int32_t* qzeros, const void* scale
                 int64_t K, int64_t N, int64_t G, void* w_out, awq_stream_t stream);
 
 /* Same result from the repacked buffers, computed by Dq<>::word, the
- * dequantisation routine of the prefill kernel (tiled_kernel), the grouped
- * MoE kernel and the bf16 GEMV path (proves their in-kernel dequantisation is
- * bit-exact).  The fp16 decode paths feed the MFMAs the exact integers q - z
+ * dequantisation routine of the prefill kernels (tiled_kernel, mfma32_kernel),
+ * the k-slice decode kernel, the grouped MoE kernel and the bf16 GEMV path
+ * (proves their in-kernel dequantisation is bit-exact).  The fp16 decode paths feed the MFMAs the exact integers q - z
  * (GEMV, 4+ rows) or the biased nibbles 1024 + q (GEMV up to 3 rows and the
  * skinny kernel) and apply the group scale to the fp32 sums instead; their
  * outputs are checked against the oracle within the GEMM tolerance. */
