@@ -229,6 +229,38 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     xr[r] = ld_off<u32x4>(x, ((uint32_t)m * (uint32_t)K + (uint32_t)k) * 2u);
   }
 
+  // ---- publish the activation slice ----------------------------------------
+  // With the biased operand, also the sum of every (row, k-tile) of the
+  // slice, xsum[kt * M + m]: the 16 chunks of one row's k-tile are 16
+  // consecutive threads (an aligned quarter wave, as cpr and NTHREADS are
+  // multiples of 16).
+  _Float16* xs = (_Float16*)smem;
+  float* xsum = (float*)((char*)smem + ((M * rs * 2 + 15) & ~15));
+  // Published before the weight loads are issued when every wave owns five or
+  // more k-tiles: the CU issues vector-memory instructions at ~24 cycles
+  // each, so a barrier after all of them (up to 512 per CU) kept every
+  // k-tile's compute until after the data had arrived (Qwen3-4B gate_up at
+  // M = 8: 11.8 -> 10.6 us, Llama-3-8B down at M = 1: 12.2 -> 11.6 us).  With
+  // fewer k-tiles per wave the weights' earlier issue is worth more (the
+  // order reversed there was 7-13% slower at M = 1).
+  constexpr bool kEarlyPublish = KPW >= 5;
+  auto publish = [&]() {
+#pragma unroll
+    for (int r = 0; r < XPT; ++r) {
+      const int qi = threadIdx.x + r * NTHREADS;
+      const bool live = qi < M * cpr;
+      const int m = live ? qi / cpr : 0, kk = live ? (qi % cpr) * 8 : 0;
+      const u32x4 v = live && kt_begin * 128 + kk < K ? xr[r] : u32x4{0u, 0u, 0u, 0u};
+      if (live) *(u32x4*)(xs + m * rs + kk) = v;
+      if constexpr (BIASED) {
+        const float sum = row16_sum(chunk_sum<DT>(v));
+        if (live && (qi & 15) == 15) xsum[(kk >> 7) * M + m] = sum;
+      }
+    }
+    __syncthreads();
+  };
+  if constexpr (kEarlyPublish) publish();
+
   // ---- weights, zero words and scales of every k-tile of this wave ---------
   // (one quantisation group per 128-row tile: G >= 128)
   u32x4 q[KPW][NTW];
@@ -264,26 +296,7 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     }
   }
 
-  // ---- publish the activation slice ----------------------------------------
-  // With the biased operand, also the sum of every (row, k-tile) of the
-  // slice, xsum[kt * M + m]: the 16 chunks of one row's k-tile are 16
-  // consecutive threads (an aligned quarter wave, as cpr and NTHREADS are
-  // multiples of 16).
-  _Float16* xs = (_Float16*)smem;
-  float* xsum = (float*)((char*)smem + ((M * rs * 2 + 15) & ~15));
-#pragma unroll
-  for (int r = 0; r < XPT; ++r) {
-    const int qi = threadIdx.x + r * NTHREADS;
-    const bool live = qi < M * cpr;
-    const int m = live ? qi / cpr : 0, kk = live ? (qi % cpr) * 8 : 0;
-    const u32x4 v = live && kt_begin * 128 + kk < K ? xr[r] : u32x4{0u, 0u, 0u, 0u};
-    if (live) *(u32x4*)(xs + m * rs + kk) = v;
-    if constexpr (BIASED) {
-      const float sum = row16_sum(chunk_sum<DT>(v));
-      if (live && (qi & 15) == 15) xsum[(kk >> 7) * M + m] = sum;
-    }
-  }
-  __syncthreads();
+  if constexpr (!kEarlyPublish) publish();
 
   // ---- compute ---------------------------------------------------------------
   // bf16 (not biased): per k-block the weights are dequantised to (q - z) * s
