@@ -236,14 +236,16 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
   // multiples of 16).
   _Float16* xs = (_Float16*)smem;
   float* xsum = (float*)((char*)smem + ((M * rs * 2 + 15) & ~15));
-  // Published before the weight loads are issued when every wave owns five or
-  // more k-tiles: the CU issues vector-memory instructions at ~24 cycles
-  // each, so a barrier after all of them (up to 512 per CU) kept every
-  // k-tile's compute until after the data had arrived (Qwen3-4B gate_up at
-  // M = 8: 11.8 -> 10.6 us, Llama-3-8B down at M = 1: 12.2 -> 11.6 us).  With
-  // fewer k-tiles per wave the weights' earlier issue is worth more (the
-  // order reversed there was 7-13% slower at M = 1).
-  constexpr bool kEarlyPublish = KPW >= 5;
+  // Published after the first k-tile's weight loads are issued and before the
+  // rest: the CU issues vector-memory instructions at ~24 cycles each, so a
+  // barrier after all of them (up to 512 per CU) kept every k-tile's compute
+  // until after the data had arrived.  Now the k-tiles are computed as their
+  // weights land (Qwen3-4B gate_up at M = 8 11.9 -> 10.3 us, qkv 7.2 -> 6.7
+  // us; Llama-3-8B down at M = 1 12.2 -> 10.9 us).  Plain GEMMs of up to 3 rows
+  // with at most 4 k-tiles per wave still issue every load first (their short
+  // launches gain more from the weights' earlier issue: o_proj at M = 1 was
+  // 3.5% slower the other way).
+  constexpr int kEarlyKt = BIASED && KPW <= 4 ? KPW : 1;  // k-tiles whose loads precede the publish
   auto publish = [&]() {
 #pragma unroll
     for (int r = 0; r < XPT; ++r) {
@@ -259,7 +261,6 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     }
     __syncthreads();
   };
-  if constexpr (kEarlyPublish) publish();
 
   // ---- weights, zero words and scales of every k-tile of this wave ---------
   // (one quantisation group per 128-row tile: G >= 128)
@@ -279,9 +280,8 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
     woff[j] = (ntc * (uint32_t)KT * 64u + lane) * 16u;
     goff[j] = ntc * (uint32_t)NG;
   }
-#pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    // k-tiles past the wave's share reload its last one (no branch around loads)
+  // k-tiles past the wave's share reload its last one (no branch around loads)
+  auto load_kt = [&](int i) {
     const int kt = kt_begin + wk + WK * min(i, max(kpw - 1, 0));
     const int ktl = min(kt, KT - 1);
     const uint32_t g = (uint32_t)min((ktl * 128) >> gshift, NG - 1);
@@ -294,9 +294,12 @@ __global__ __launch_bounds__(64 * WN * WK) void gemv_kernel(
       if constexpr (BIASED || std::is_same_v<DT, F16>)
         s4[i][j] = ld_off<uint2>(s_r, (gi * 16u + 4u * (uint32_t)lg) * 2u);
     }
-  }
-
-  if constexpr (!kEarlyPublish) publish();
+  };
+#pragma unroll
+  for (int i = 0; i < kEarlyKt; ++i) load_kt(i);
+  publish();
+#pragma unroll
+  for (int i = kEarlyKt; i < KPW; ++i) load_kt(i);
 
   // ---- compute ---------------------------------------------------------------
   // bf16 (not biased): per k-block the weights are dequantised to (q - z) * s
