@@ -156,9 +156,13 @@ __global__ __launch_bounds__(256, 2) void kslice_kernel(KsArgs a) {
   const uint32_t zshift = 4u * (uint32_t)(c & 7);
   const int ktw = kt0 + wk * KPW;  // this wave's first k-tile
 
+  // Issue order: the slice's activation rows (LDS-DMA), the first k-tile's
+  // weights, then -- once this wave's DMAs have landed (the loads complete in
+  // order: everything but the first k-tile's) and every wave has met -- the
+  // other k-tiles' weights, so that each k-tile is multiplied as its weights
+  // land instead of after the last of them.
   WStage32<GPT> stg[KPW];
-#pragma unroll
-  for (int p = 0; p < KPW; ++p) {
+  auto load_w = [&](int p) {
     const int kt = min(ktw + p, KT - 1);
     const bool live = ktw + p < kend;
     const int g0 = (kt * 128) >> a.gshift;
@@ -174,11 +178,18 @@ __global__ __launch_bounds__(256, 2) void kslice_kernel(KsArgs a) {
       for (int q = 0; q < GPT; ++q)
         stg[p].s[g][q] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[g] + 32 * q, g0 * 32, 0);
     }
-  }
+  };
+  constexpr int kLoadsKt = 2 * (2 + 2 * GPT);  // load instructions per k-tile
   load_x();
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(0);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoadsKt));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+#pragma unroll
+  for (int p = 1; p < KPW; ++p) load_w(p);
 
   // ---- multiply ---------------------------------------------------------------
   f32x16 acc[2];
