@@ -589,16 +589,20 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
 // heavy groups meeting on one CU by chance.  Each wave ranks the groups
 // itself (one lane per group, ballots); the result is the logical group
 // index, or -1 for a local index with no group.  Placement other than assumed
-// changes only the balance, never the result.
-__device__ __forceinline__ int balanced_group(const MoeArgs& a, int xcd, int per, int j, int lane) {
+// changes only the balance, never the result.  The chosen group's row range
+// [r0, r1) comes back with it (the lane that ranked it has loaded it), which
+// spares the workgroup a dependent load before its rows can be fetched.
+__device__ __forceinline__ int balanced_group(const MoeArgs& a, int xcd, int per, int j, int lane, int& g_r0,
+                                              int& g_r1) {
   const int L = xcd * per + lane;
   int key = -1;  // lanes past the XCD's groups take no rank
+  int r0 = 0, r1 = 0;
   if (lane < per) {
     key = 0;
     if (L < a.total) {
       const int e = L / a.SG;
-      const int r0 = min(max(a.offsets[e], 0), a.sorted_cap);
-      const int r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
+      r0 = min(max(a.offsets[e], 0), a.sorted_cap);
+      r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
       key = min((r1 - r0) >> 4, kMaxMt);
     }
   }
@@ -611,7 +615,11 @@ __device__ __forceinline__ int balanced_group(const MoeArgs& a, int xcd, int per
   }
   const int r = j < a.cpx ? j : per - 1 - (j - a.cpx);
   const uint64_t hit = __ballot(key >= 0 && rank == r);
-  return hit ? xcd * per + __builtin_ctzll(hit) : -1;
+  if (!hit) return -1;
+  const int src = __builtin_ctzll(hit);
+  g_r0 = __builtin_amdgcn_readlane(r0, src);
+  g_r1 = __builtin_amdgcn_readlane(r1, src);
+  return xcd * per + src;
 }
 
 template <int TW, int GPT, int EPI, int NS, typename DT>
@@ -623,14 +631,16 @@ __global__ __launch_bounds__(kThreads, 2) void moe_gemm_kernel(MoeArgs a) {
   // paired heavy with light on its CUs.
   const int per = gridDim.x >> 3, xcd = blockIdx.x & 7, j = blockIdx.x >> 3;
   const int lane = threadIdx.x & 63;
-  const int L = gridDim.y == 1 && per > a.cpx && per <= 2 * a.cpx && per <= 64
-                    ? balanced_group(a, xcd, per, j, lane)
-                    : xcd * per + j;
+  const bool balanced = gridDim.y == 1 && per > a.cpx && per <= 2 * a.cpx && per <= 64;
+  int r0 = 0, r1 = 0;
+  const int L = balanced ? balanced_group(a, xcd, per, j, lane, r0, r1) : xcd * per + j;
   if (L < 0 || L >= a.total) return;
   const int e = L / a.SG, grp = L % a.SG;
   const int u0 = grp * a.U, units = min(a.U, a.S - u0);
-  const int r0 = min(max(a.offsets[e], 0), a.sorted_cap);
-  const int r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
+  if (!balanced) {
+    r0 = min(max(a.offsets[e], 0), a.sorted_cap);
+    r1 = min(max(a.offsets[e + 1], r0), a.sorted_cap);
+  }
   const int nblk = (r1 - r0) >> 4;
   if ((int)blockIdx.y * kMaxMt >= nblk) return;
 
