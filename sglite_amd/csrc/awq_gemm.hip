@@ -397,19 +397,33 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // scales come from LDS also at 12-16 k-slices: Llama-3-8B down at M = 12,
     // 16, 32 15.6 -> 14.1, 15.7 -> 14.6, 17.2 -> 16.9 us).
     if (!env_bm_ok && best_bm == 32 && g.G >= 128) best_bm = 4032;
-    if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64 &&
-        ((g.NT + 15) / 16) * ((g.M + 127) / 128) * 2 >= 3 * (int64_t)g.cus)
-      best_bm = 2128;
     // One 8-wave workgroup of 512 columns per CU instead of two of 256: the
     // CU's columns share one activation stage (half the activation loads
     // per weight byte), and a grid of at most one round, or of whole rounds,
     // of 512-column tiles keeps every CU equally loaded where 256-column
     // tiles would double up on some CUs only (Llama-3-8B qkv at M = 2048:
     // 129 -> 112 us; qkv, o and down at M = 8192: 2-3% faster; gate_up at
-    // M = 2048, 3.5 rounds, stays faster with two workgroups per CU).
-    if (!env_bm_ok && best_bm == 2128 && g.G >= 128) {
+    // M = 2048, 3.5 rounds, stays faster with two workgroups per CU; at
+    // M = 1024, whose last round is three quarters full, 232 -> 220 us).
+    // Above 256 rows, a grid of less than one round of 128 x 256 tiles takes
+    // the 32x32-MFMA kernel at one workgroup per CU (Llama-3-8B and Qwen3-4B
+    // qkv at M = 1024: 65.0 -> 59.2 and 44.6 -> 40.8 us; Qwen3-4B o_proj at
+    // M = 2048: 63.3 -> 56.0 us; on exactly one round both kinds tie), and
+    // one of between one and one and a half rounds the 8-wave kernel when its
+    // 512-column tiles fit one round (Qwen3-4B gate_up at M = 512, 304
+    // tiles: 86.0 -> 60.6 us).
+    if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64) {
+      const int64_t t2 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
       const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 127) / 128);
-      if (t8 <= g.cus || t8 % g.cus == 0) best_bm = 8128;
+      const int64_t cus = g.cus;
+      if (2 * t2 >= 3 * cus) {
+        best_bm = 2128;
+        if (g.G >= 128 && (t8 <= cus || t8 % cus == 0 || 4 * (t8 % cus) >= 3 * cus)) best_bm = 8128;
+      } else if (g.M > 256 && t2 < cus) {
+        best_bm = 2128;
+      } else if (g.M > 256 && g.G >= 128 && t2 > cus && t8 <= cus) {
+        best_bm = 8128;
+      }
     }
     // Batches of up to 256 rows with K unsplit, one group per k-tile
     // (graph-replay sweep of the Qwen3-4B and Llama-3-8B linears at M =

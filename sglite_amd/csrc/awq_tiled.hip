@@ -562,6 +562,17 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   constexpr bool kZsLds = NS * GPT <= 6;
   using ZC = ZsChunks<NW>;
   constexpr int kLoadsW = kZsLds ? 4 : 4 + 4 * GPT;  // weight-stage load instructions per k-tile
+  // 128-row blocks issue a step's activation DMAs and weight loads spread
+  // over the k-tile's eight k-steps (same order, so the same waits), not in
+  // one burst before its first MFMA: the eight waves of a CU issue ~12 such
+  // loads per k-tile each, the CU accepts one every ~24 cycles, and a wave
+  // whose load waits in that queue cannot issue its MFMAs.  Between k-steps
+  // the wait overlaps the MFMAs in flight (Llama-3-8B gate_up at M = 2048
+  // 453 -> 434 us, Qwen3-4B down at M = 8192 424 -> 389 us; 32- and 64-row
+  // forms, four or more waves per SIMD's worth of loads already in flight,
+  // measured no gain and keep the burst).
+  constexpr bool kSpread = kZsLds && BM >= 128;
+  constexpr int kNL = XPW + kLoadsW;  // loads per step when spread
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
   static_assert(kAfterX < 64, "vector-memory counter range");
   __shared__ u32x4 xs0[XF * 64];
@@ -648,15 +659,22 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][g][e] = 0.f;
 
+  auto load_x1 = [&](int p, int kt, int j) {
+    const int f = wave * XPW + j, st = f & 7;
+    const bool kval = kt < kend && kt * 128 + st * 16 < K;  // wave-uniform
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
+    load_lds16(r, &xbuf(p)[f * 64], xoff[j], kt * 256);
+  };
   auto load_x = [&](int p, int kt) {
-    u32x4* dst = xbuf(p);
 #pragma unroll
-    for (int j = 0; j < XPW; ++j) {
-      const int f = wave * XPW + j, st = f & 7;
-      const bool kval = kt < kend && kt * 128 + st * 16 < K;  // wave-uniform
-      const __amdgpu_buffer_rsrc_t r = make_rsrc(xb, kval ? xbytes : 0u);
-      load_lds16(r, &dst[f * 64], xoff[j], kt * 256);
-    }
+    for (int j = 0; j < XPW; ++j) load_x1(p, kt, j);
+  };
+  // Weight vector i (group i / 2, odd-step half i % 2) of k-tile kt.
+  auto load_w1 = [&](WStage32<GPT>& S, int kt, int i) {
+    const bool live = kt < kend;
+    kt = min(kt, KT - 1);
+    const int g = i >> 1, hf = i & 1;
+    S.q[g][hf] = __builtin_amdgcn_raw_buffer_load_b128(live ? wr[g] : r0, woff[g] + 512u * hf, kt * 1024, 0);
   };
   auto load_w = [&](WStage32<GPT>& S, int kt) {
     const bool live = kt < kend;
@@ -697,7 +715,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   // dequantisation of step s + 1 are issued between step s's MFMAs (one LDS
   // read and a few vector operations after each MFMA), so no MFMA waits for
   // an operand produced just before it.
-  auto compute = [&](const WStage32<GPT>& S, const u32x4* xsb) {
+  auto compute = [&](const WStage32<GPT>& S, const u32x4* xsb, auto&& hook) {
     ZS zs[2][GPT];
 #pragma unroll
     for (int g = 0; g < 2; ++g)
@@ -711,6 +729,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     for (int g = 0; g < 2; ++g) av[0][g] = Dq<DT>::word(S.q[g][0][0], zs[g][0], dk);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
+      hook(st);
       const int cur = st & 1, nxt = cur ^ 1;
       if (st + 1 < 8) {
         const int sn = st + 1;
@@ -773,17 +792,30 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
       if (p == 1) dma_chunk((kt - 1 - kt0) / NS + 2);
       __builtin_amdgcn_sched_barrier(0);
     }
-    load_x(pa, kt + NS - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(stg[pa], kt + NS - 1);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (kZsLds) {
-      // Issued before the compute's LDS reads, whose waits then cover them
-      // before the barrier after which a chunk buffer may be refilled.
+    if constexpr (kSpread) {
       read_zs(stg[pa], kt + NS - 1);
       __builtin_amdgcn_sched_barrier(0);
+      compute(stg[p], xbuf(p), [&](int st) {
+#pragma unroll
+        for (int l = st * kNL / 8; l < (st + 1) * kNL / 8; ++l) {
+          if (l < XPW) load_x1(pa, kt + NS - 1, l);
+          else load_w1(stg[pa], kt + NS - 1, l - XPW);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+      load_x(pa, kt + NS - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(stg[pa], kt + NS - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kZsLds) {
+        // Issued before the compute's LDS reads, whose waits then cover them
+        // before the barrier after which a chunk buffer may be refilled.
+        read_zs(stg[pa], kt + NS - 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      compute(stg[p], xbuf(p), [](int) {});
     }
-    compute(stg[p], xbuf(p));
     sync_step();
   };
   int i = 0;

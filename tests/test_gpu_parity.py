@@ -214,8 +214,23 @@ def test_qwen3_4b_layer_decode(K, N, M):
     _check_full_size(y, W, x, t, K, N)
 
 
+@pytest.mark.parametrize("K,N", QWEN3_4B)
+@pytest.mark.parametrize("M", [512, 2048])
+def test_qwen3_4b_prefill_sizes(K, N, M):
+    """Qwen3-4B linears at prefill chunk sizes whose grids are under one round
+    or between one and one and a half rounds of 128 x 256 tiles (the planner
+    routes them to the one-workgroup 32x32 and the 8-wave forms)."""
+    ops = _ops()
+    t, d = _linear(K, N, 128, seed=K + N)
+    r = ops.repack(d["qweight"], d["qzeros"], d["scales"])
+    W = ops.dequant_repacked(r, K, N, 128)
+    x = oracle.make_activation(M, K, seed=300 + M)
+    y = ops.gemm(x.to(DEV), r, K, N, 128, counters=ops.make_counters(N, DEV))
+    _check_full_size(y, W, x, t, K, N)
+
+
 @pytest.mark.parametrize("K,N", LLAMA3_8B)
-@pytest.mark.parametrize("M", [1, 8, 16, 64, 128, 160, 256, 2048, 8192])
+@pytest.mark.parametrize("M", [1, 8, 16, 64, 128, 160, 256, 1024, 2048, 8192])
 def test_llama3_8b_shapes(K, N, M):
     """Config 2 at every M it names, up to the reference's largest prefill chunk
     (max_extend_tokens = 8192, scheduler/config.py:20), and the decode batches

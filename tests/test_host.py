@@ -244,6 +244,11 @@ def test_plan_overrides_and_plan_info():
     (2048, 6144, 4096, 8128, 1, 192),    # at most one round of 512-column tiles
     (2048, 4096, 4096, 128, 1, 256),     # one round of 256-column tiles
     (8192, 28672, 4096, 8128, 1, 3584),  # whole rounds
+    (1024, 28672, 4096, 8128, 1, 448),   # last round of 512-column tiles three quarters full
+    (2048, 19456, 2560, 2128, 1, 1216),  # last round a quarter full: two workgroups per CU
+    (1024, 6144, 4096, 2128, 1, 192),    # under one round: 32x32 kernel, one workgroup per CU
+    (2048, 2560, 4096, 2128, 1, 160),
+    (512, 19456, 2560, 8128, 1, 152),    # 1.2 rounds of 256-column tiles, 0.6 of 512-column ones
 ])
 def test_tiled_plan_forms(M, N, K, variant, ks, wgs):
     """The planner's row-block form per batch size on a whole MI355X (256 CUs, the
