@@ -381,12 +381,13 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   // (the K tail and the padding k-tiles) read at offset x_bytes, outside the
   // buffer, which returns zeros.
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.x_bytes);
-  auto dma_x = [&](int kt, int slot) {
+  auto dma_x1 = [&](int kt, int slot, int mt) {
     const int k0 = kt * 128 + wave * 32;
-    u32x4* dst = xs + slot * FR * 64;
+    load_lds16(xr, xs + (slot * FR + mt * 4 + wave) * 64, k0 < a.K ? xrow[mt] + (uint32_t)k0 * 2u : a.x_bytes, 0);
+  };
+  auto dma_x = [&](int kt, int slot) {
 #pragma unroll
-    for (int mt = 0; mt < MC; ++mt)
-      load_lds16(xr, dst + (mt * 4 + wave) * 64, k0 < a.K ? xrow[mt] + (uint32_t)k0 * 2u : a.x_bytes, 0);
+    for (int mt = 0; mt < MC; ++mt) dma_x1(kt, slot, mt);
   };
 
   f32x4 acc[MC][TW];
@@ -420,24 +421,26 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
     uint32_t z[TW][GPT];  // zero-point word holding the lane's nibble
     uint16_t s[TW][GPT];  // scale bits (kept 16-bit: a widening would wait for the load at once)
   };
+  // Load l of a k-tile's LW (in issue order: the TW weight vectors, then per
+  // group each tile's zero word and scale).
+  auto load_w1 = [&](int u, int kt, Stage& st, int l) {
+    if (l < TW) {
+      st.q[l] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[l], u * wsh + kt * 1024, kCacheStream);
+    } else {
+      const int r = l - TW, gg = r / (2 * TW), j = (r % (2 * TW)) >> 1;
+      const int g = min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
+      if (r & 1) st.s[j][gg] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], u * ssh + g * 32, 0);
+      else st.z[j][gg] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j], u * zsh + g * 8, 0);
+    }
+  };
   auto load_w = [&](int u, int kt, Stage& st) {
 #pragma unroll
-    for (int j = 0; j < TW; ++j)
-      st.q[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, woff[j], u * wsh + kt * 1024, kCacheStream);
-#pragma unroll
-    for (int gg = 0; gg < GPT; ++gg) {
-      const int g = min((kt * 128 + 32 * BPG * gg) >> a.gshift, a.NG - 1);
-#pragma unroll
-      for (int j = 0; j < TW; ++j) {
-        st.z[j][gg] = __builtin_amdgcn_raw_buffer_load_b32(zr, zoff[j], u * zsh + g * 8, 0);
-        st.s[j][gg] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[j], u * ssh + g * 32, 0);
-      }
-    }
+    for (int l = 0; l < TW * (1 + 2 * GPT); ++l) load_w1(u, kt, st, l);
   };
   // One k-tile: the activation operands and dequantised weights of k-block
   // w + 1 are fetched while k-block w's MFMAs run (operands double-buffered),
   // so no MFMA waits for an LDS read or a dequantisation issued just before.
-  auto compute = [&](const Stage& st, const u32x4* buf) {
+  auto compute = [&](const Stage& st, const u32x4* buf, auto&& hook) {
     ZS zs[TW][GPT];
 #pragma unroll
     for (int gg = 0; gg < GPT; ++gg)
@@ -450,6 +453,7 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
     for (int j = 0; j < TW; ++j) av[0][j] = Dq<DT>::word(st.q[j][0], zs[j][0], dk);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {  // k-blocks past K meet zeroed activations
+      hook(w);
       const int cur = w & 1, nxt = cur ^ 1;
       if (w + 1 < 4) {
 #pragma unroll
@@ -536,18 +540,30 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   // and the steps past the last slice load what the buffer ranges allow and
   // are never multiplied.  A slice's epilogue runs between loop iterations
   // (its stores only make later waits stricter).
-  constexpr int LW = TW * (1 + 2 * GPT);           // weight, zero and scale loads per k-tile
-  constexpr int kInFlight = (NS - 1) * (MC + LW);  // loads of the NS - 1 newer steps
+  constexpr int LW = TW * (1 + 2 * GPT);  // weight, zero and scale loads per k-tile
+  // With NS >= 3 a step's loads (of step s + NS - 1) are issued spread over
+  // the four k-blocks of step s's multiply instead of in one burst before it:
+  // the CU accepts a vector-memory instruction every ~24 cycles, and a wave
+  // whose load waits behind the other seven waves' cannot issue its MFMAs.
+  // Its wait then leaves NS - 2 newer steps in flight (gate_up 69.8 -> 67.6
+  // us, down 40.8 -> 39.7 us on the Qwen3-30B-A3B shape).  The slot a DMA
+  // fills was last read at step s + NS - 1 - R <= s - 2, before the barrier
+  // that starts step s.
+  constexpr bool kSpread = NS >= 3;
+  constexpr int kInFlight = (kSpread ? NS - 2 : NS - 1) * (MC + LW);  // loads of the newer steps
   static_assert(kInFlight <= 63, "vmcnt holds at most 63");
   const int KTp = (KT + NS - 1) / NS * NS;
   const int nsteps = units * KTp;
   int iu = 0, ik = 0, islot = 0;  // next step to issue: slice, k-tile, ring slot
-  auto issue = [&](Stage& st) {
-    dma_x(ik, islot);
-    load_w(iu, min(ik, KT - 1), st);
+  auto advance = [&]() {
     islot = islot + 1 == R ? 0 : islot + 1;
     ik = ik + 1 == KTp ? 0 : ik + 1;
     iu = ik == 0 ? iu + 1 : iu;
+  };
+  auto issue = [&](Stage& st) {
+    dma_x(ik, islot);
+    load_w(iu, min(ik, KT - 1), st);
+    advance();
   };
   Stage st[NS];
   // The prologue issues in the steady-state order (an empty asm statement
@@ -563,12 +579,30 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   for (int s = 0; s < nsteps; s += NS) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      issue(st[(i + NS - 1) % NS]);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's math
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(kInFlight));
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      compute(st[i], xs + cslot * FR * 64);
+      Stage& sn = st[(i + NS - 1) % NS];
+      if constexpr (kSpread) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kInFlight));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int kt = min(ik, KT - 1);
+        compute(st[i], xs + cslot * FR * 64, [&](int w) {
+          constexpr int NL = MC + LW;
+#pragma unroll
+          for (int l = w * NL / 4; l < (w + 1) * NL / 4; ++l) {
+            if (l < MC) dma_x1(ik, islot, l);
+            else load_w1(iu, kt, sn, l - MC);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        advance();
+      } else {
+        issue(sn);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this tile's math
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kInFlight));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        compute(st[i], xs + cslot * FR * 64, [](int) {});
+      }
       cslot = cslot + 1 == R ? 0 : cslot + 1;
     }
     ck += NS;
