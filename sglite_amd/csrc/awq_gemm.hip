@@ -352,8 +352,11 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // columns and 8192 rows of K (graph-replay A/B at M = 48..160 over the
     // Llama-3-8B and Qwen3-4B linears: qkv and o 7-19% faster in the 32x32
     // kernel with four workgroups per CU; wider or deeper layers, gate_up and
-    // down, 3-16% slower, so they keep 64- and 128-row blocks).
-    const bool bm32_ok = g.M <= 32 || (g.M <= 160 && g.N <= 8192 && g.K <= 8192);
+    // down, 3-16% slower, so they keep 64- and 128-row blocks), and up to 112
+    // rows on layers of at most 4096 columns and 12288 rows of K (Qwen3-4B
+    // down at M = 40..112: 5-10% faster; even at 128, slower at 160).
+    const bool bm32_ok = g.M <= 32 || (g.M <= 160 && g.N <= 8192 && g.K <= 8192) ||
+                         (g.M <= 112 && g.N <= 4096 && g.K <= 12288);
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
                            env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128;

@@ -215,11 +215,12 @@ def test_qwen3_4b_layer_decode(K, N, M):
 
 
 @pytest.mark.parametrize("K,N", QWEN3_4B)
-@pytest.mark.parametrize("M", [512, 2048])
+@pytest.mark.parametrize("M", [64, 96, 512, 2048])
 def test_qwen3_4b_prefill_sizes(K, N, M):
-    """Qwen3-4B linears at prefill chunk sizes whose grids are under one round
-    or between one and one and a half rounds of 128 x 256 tiles (the planner
-    routes them to the one-workgroup 32x32 and the 8-wave forms)."""
+    """Qwen3-4B linears at mid-size batches (the down projection in 32-row
+    blocks with split K) and at prefill chunk sizes whose grids are under one
+    round or between one and one and a half rounds of 128 x 256 tiles (the
+    planner routes them to the one-workgroup 32x32 and the 8-wave forms)."""
     ops = _ops()
     t, d = _linear(K, N, 128, seed=K + N)
     r = ops.repack(d["qweight"], d["qzeros"], d["scales"])

@@ -249,6 +249,10 @@ def test_plan_overrides_and_plan_info():
     (1024, 6144, 4096, 2128, 1, 192),    # under one round: 32x32 kernel, one workgroup per CU
     (2048, 2560, 4096, 2128, 1, 160),
     (512, 19456, 2560, 8128, 1, 152),    # 1.2 rounds of 256-column tiles, 0.6 of 512-column ones
+    (64, 2560, 9728, 4032, 11, 220),     # Qwen3-4B down: 32-row blocks up to 112 rows at K <= 12288
+    (112, 2560, 9728, 4032, 6, 240),
+    (128, 2560, 9728, 64, 11, 220),
+    (64, 4096, 14336, 64, 16, 256),      # Llama-3-8B down (K = 14336) keeps 64-row blocks
 ])
 def test_tiled_plan_forms(M, N, K, variant, ks, wgs):
     """The planner's row-block form per batch size on a whole MI355X (256 CUs, the
