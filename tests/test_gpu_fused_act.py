@@ -62,6 +62,8 @@ def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env
     (16, 1024, 9728, "skinny_kernel"),  # wide: two-tile shapes by default
     (40, 2048, 1040, "tiled_kernel"),   # split K
     (300, 1024, 528, "tiled_kernel"),
+    (1024, 2560, 2080, "tiled_kernel"),  # under one round of 128 x 256 tiles: 32x32 kernel, one workgroup per CU
+    (512, 1024, 9728, "tiled_kernel"),   # 1.2 rounds of them, 0.6 of 512-column tiles: the 8-wave kernel
 ])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fused_silu_matches_oracle(M, K, I, kernel, dtype, plan):

@@ -263,6 +263,16 @@ def test_tiled_plan_forms(M, N, K, variant, ks, wgs):
     assert (info.kernel, info.variant, info.k_slices, info.workgroups) == ("tiled_kernel", variant, ks, wgs)
 
 
+def test_tiled_plan_forms_with_fused_activation():
+    """The fused gate/up GEMM takes the same row-block forms as the plain one
+    at prefill sizes (the gated pairs stay within a workgroup in each form)."""
+    if ops.device_cu_count() != 256:
+        pytest.skip("the forms are pinned for a whole MI355X (256 CUs)")
+    for M, N, K, variant in [(1024, 4160, 2560, 2128), (512, 19456, 1024, 8128), (2048, 19456, 2560, 2128)]:
+        assert ops.plan_info(M, N, K, 128, "silu").variant == variant, (M, N, K)
+        assert ops.plan_info(M, N, K, 128).variant == variant, (M, N, K)
+
+
 def test_stream_probe_validates_before_launch():
     lib = _lib.load()
     fake = 0x10000
