@@ -359,12 +359,13 @@ GemmPlan plan_gemm(const Geom& g, int act) {
                          (g.M <= 112 && g.N <= 4096 && g.K <= 12288);
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
-                           env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128;
+                           env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128 ||
+                           (env_bm == 9128 && g.G >= 64);
     const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128}) {
+    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9128}) {
       const int bm = code % 1000;
       if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
       if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && !bm32_ok)) continue;
@@ -408,15 +409,28 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 129 -> 112 us; qkv, o and down at M = 8192: 2-3% faster; gate_up at
     // M = 2048, 3.5 rounds, stays faster with two workgroups per CU; at
     // M = 1024, whose last round is three quarters full, 232 -> 220 us).
-    // Above 256 rows, a grid of less than one round of 128 x 256 tiles takes
-    // the 32x32-MFMA kernel at one workgroup per CU (Llama-3-8B and Qwen3-4B
-    // qkv at M = 1024: 65.0 -> 59.2 and 44.6 -> 40.8 us; Qwen3-4B o_proj at
-    // M = 2048: 63.3 -> 56.0 us; on exactly one round both kinds tie), and
-    // one of between one and one and a half rounds the 8-wave kernel when its
-    // 512-column tiles fit one round (Qwen3-4B gate_up at M = 512, 304
-    // tiles: 86.0 -> 60.6 us).
+    // Above 256 rows, an unsplit grid of at most half a round of 128 x 256
+    // tiles (more goes to code 9128 below) takes the 32x32-MFMA kernel at one
+    // workgroup per CU (on grids of 160-192 tiles it was 8-11% faster than
+    // the 16x16 kernel: Llama-3-8B and Qwen3-4B qkv at M = 1024 65.0 -> 59.2
+    // and 44.6 -> 40.8 us), and one of between one and one and a half rounds
+    // the 8-wave kernel when its 512-column tiles fit one round (Qwen3-4B
+    // gate_up at M = 512, 304 tiles: 86.0 -> 60.6 us).
+    // Above 256 rows, a grid of more than half and at most one round of
+    // 128 x 256 tiles runs the 32x32-MFMA kernel with 8 waves that split each
+    // k-tile's k-steps in two (code 9128: two waves per SIMD on a one-
+    // workgroup-per-CU grid, K unsplit): Qwen3-4B down at M = 2048 120.1 (3
+    // k-slices) -> 110.5 us, o_proj 60.8 -> 55.2 us; Llama-3-8B o at M = 2048
+    // 73.0 -> 70.0 us, qkv at M = 1024 61.4 -> 59.1 us; 70B-sized qkv at
+    // M = 512 105.3 -> 98.0 us, o at M = 1024 128.0 -> 124.9 us; Llama-3-8B
+    // down at M = 2048 ties.  On half a round or less the split-K plans win.
+    const int64_t t2_128 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
+    if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 256 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
+      best_bm = 9128;
+      ks = 1;
+    }
     if (!env_bm_ok && best_bm == 128 && ks == 1 && g.G >= 64) {
-      const int64_t t2 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
+      const int64_t t2 = t2_128;
       const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 127) / 128);
       const int64_t cus = g.cus;
       if (2 * t2 >= 3 * cus) {
@@ -443,7 +457,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
       else if (best_bm == 64) best_bm = 2064;
     }
     p.variant = best_bm;
-    p.grid_x = best_bm >= 8000 ? (g.NT + 31) / 32 : (g.NT + 15) / 16;
+    p.grid_x = best_bm >= 8000 && best_bm < 9000 ? (g.NT + 31) / 32 : (g.NT + 15) / 16;
     p.grid_y = (g.M + best_bm % 1000 - 1) / (best_bm % 1000);
     p.ktc = (int)((g.KT + ks - 1) / ks);
     p.ks = (int)((g.KT + p.ktc - 1) / p.ktc);  // every slice gets >= 1 k-tile

@@ -547,7 +547,7 @@ hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, 
 // output columns 8 j + 4 (l / 32) .. + 3 (j = 0..3) of its column group.
 // ---------------------------------------------------------------------------
 
-template <int BM, int GPT, int NS, int OCC, int NW, typename DT>
+template <int BM, int GPT, int NS, int OCC, int NW, typename DT, int KW = 1>
 __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   using E = typename DT::elem;
   using V8 = typename DT::vec8;
@@ -560,8 +560,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   // LDS in ZsChunks, one chunk per NS k-tiles, double-buffered; otherwise each
   // stage loads them (4 GPT loads per wave).
   constexpr bool kZsLds = NS * GPT <= 6;
-  using ZC = ZsChunks<NW>;
-  constexpr int kLoadsW = kZsLds ? 4 : 4 + 4 * GPT;  // weight-stage load instructions per k-tile
+  // KW = 2: waves w and w + NW / 2 own the same columns and split every
+  // k-tile's eight k-steps, even and odd (each loads only its half of the
+  // weight vectors); their accumulators are added through LDS at the end.
+  constexpr int CW = NW / KW;  // column waves
+  static_assert(KW == 1 || (KW == 2 && kZsLds), "the k-wave split reads its zero points and scales from LDS");
+  using ZC = ZsChunks<CW>;
+  constexpr int kLoadsW = kZsLds ? 4 / KW : 4 + 4 * GPT;  // weight-stage load instructions per k-tile
+  constexpr int NST = 8 / KW;  // k-steps per k-tile of one wave
   // 128-row blocks issue a step's activation DMAs and weight loads spread
   // over the k-tile's eight k-steps (same order, so the same waits), not in
   // one burst before its first MFMA: the eight waves of a CU issue ~12 such
@@ -575,7 +581,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   constexpr int kNL = XPW + kLoadsW;  // loads per step when spread
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
   static_assert(kAfterX < 64, "vector-memory counter range");
-  __shared__ u32x4 xs0[XF * 64];
+  __shared__ u32x4 xs0[(KW == 2 ? 2 : 1) * XF * 64];  // (KW = 2: also the final exchange, 64 KiB)
   __shared__ u32x4 xs1[XF * 64];
   __shared__ u32x4 xs2[NS > 2 ? XF * 64 : 1];
   __shared__ u32x4 xs3[NS > 3 ? XF * 64 : 1];
@@ -583,6 +589,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   auto xbuf = [&](int p) -> u32x4* { return p == 0 ? xs0 : (p == 1 ? xs1 : (p == 2 ? xs2 : xs3)); };
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cw = KW == 1 ? wave : wave % CW;  // column wave
+  const int kw = KW == 1 ? 0 : wave / CW;     // k-wave: even (0) or odd (1) k-steps
   const int lane = threadIdx.x & 63;
   const int c32 = lane & 31, h = lane >> 5, c = lane & 15, t = (lane >> 4) & 1;
   const int tiles = a.gx * a.gy;
@@ -611,7 +619,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   // Weights of the wave's two column groups: group g covers slots 2g, 2g + 1
   // (with a fused gate/up activation: gate tiles t, t + 1 in group 0 and their
   // up tiles in group 1).  Tiles past the end clamp to the last tile.
-  const int nt0 = bx * (4 * NW) + wave * 4;
+  const int nt0 = bx * (4 * CW) + cw * 4;
   const int NTg = a.NT >> 1;
   const int pb0 = a.act ? (nt0 >> 1) : nt0;
   const int pb1 = a.act ? (nt0 >> 1) + NTg : nt0 + 2;
@@ -633,7 +641,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     woff[g] = dt * (uint32_t)KT * 1024u + (uint32_t)(c + 16 * h) * 16u;  // + 512 for the odd-step vector
     if constexpr (kZsLds) {
       // This lane's tile slot in a chunk, and its zero word's and scale's offsets.
-      const int u = a.act ? (g == 0 ? 0 : ZC::TPW / 2) + wave * 2 + t : wave * 4 + 2 * g + t;
+      const int u = a.act ? (g == 0 ? 0 : ZC::TPW / 2) + cw * 2 + t : cw * 4 + 2 * g + t;
       zoff[g] = ZC::zero_at(u, c);
       soff[g] = ZC::scale_at(u, c);
     } else {
@@ -646,10 +654,16 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   const __amdgpu_buffer_rsrc_t r0 = make_rsrc(a.w, 0u);
   const uint32_t zshift = 4u * (uint32_t)(c & 7);
   ZC zc;
-  if constexpr (kZsLds) zc.init(a, bx, wave, lane);
+  if constexpr (kZsLds) zc.init(a, bx, cw, lane);
   // Chunk ci: k-tiles kt0 + ci NS .. + NS - 1.
   auto chunk_g0 = [&](int ci) { return ((kt0 + ci * NS) * 128) >> a.gshift; };
-  auto dma_chunk = [&](int ci) { zc.copy(zsl[ci & 1], chunk_g0(ci), wave); };
+  auto dma_chunk = [&](int ci) {
+    if (kw == 0) zc.copy(zsl[ci & 1], chunk_g0(ci), cw);
+  };
+  // KW = 2: this wave's half of each weight vector pair (its k-steps' words).
+  uint32_t woffk[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) woffk[g] = woff[g] + 512u * (uint32_t)kw;
 
   f32x16 acc[MT][2];
 #pragma unroll
@@ -673,8 +687,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   auto load_w1 = [&](WStage32<GPT>& S, int kt, int i) {
     const bool live = kt < kend;
     kt = min(kt, KT - 1);
-    const int g = i >> 1, hf = i & 1;
-    S.q[g][hf] = __builtin_amdgcn_raw_buffer_load_b128(live ? wr[g] : r0, woff[g] + 512u * hf, kt * 1024, 0);
+    if constexpr (KW == 1) {
+      const int g = i >> 1, hf = i & 1;
+      S.q[g][hf] = __builtin_amdgcn_raw_buffer_load_b128(live ? wr[g] : r0, woff[g] + 512u * hf, kt * 1024, 0);
+    } else {
+      S.q[i][0] = __builtin_amdgcn_raw_buffer_load_b128(live ? wr[i] : r0, woffk[i], kt * 1024, 0);
+    }
   };
   auto load_w = [&](WStage32<GPT>& S, int kt) {
     const bool live = kt < kend;
@@ -683,8 +701,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const __amdgpu_buffer_rsrc_t rw = live ? wr[g] : r0;
-      S.q[g][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g], kt * 1024, 0);
-      S.q[g][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g] + 512u, kt * 1024, 0);
+      if constexpr (KW == 1) {
+        S.q[g][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g], kt * 1024, 0);
+        S.q[g][1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff[g] + 512u, kt * 1024, 0);
+      } else {
+        S.q[g][0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woffk[g], kt * 1024, 0);
+      }
       if constexpr (!kZsLds) {
         const __amdgpu_buffer_rsrc_t rz = live ? zr[g] : r0, rs = live ? sr[g] : r0;
 #pragma unroll
@@ -723,26 +745,32 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
       for (int q = 0; q < GPT; ++q) zs[g][q] = Dq<DT>::make((S.z[g][q] >> zshift) & 0xFu, S.s[g][q]);
     V8 av[2][2];
     V8 bx[2][MT];
+    // Step s of this wave is k-step KW s + kw of the k-tile.
+    const u32x4* xk = xsb + kw * 64;
+    auto word_of = [&](int g, int sn) -> uint32_t {
+      if constexpr (KW == 1) return S.q[g][sn & 1][sn >> 1];
+      else return S.q[g][0][sn];
+    };
 #pragma unroll
-    for (int i = 0; i < MT; ++i) bx[0][i] = __builtin_bit_cast(V8, xsb[i * 8 * 64 + lane]);
+    for (int i = 0; i < MT; ++i) bx[0][i] = __builtin_bit_cast(V8, xk[i * 8 * 64 + lane]);
 #pragma unroll
-    for (int g = 0; g < 2; ++g) av[0][g] = Dq<DT>::word(S.q[g][0][0], zs[g][0], dk);
+    for (int g = 0; g < 2; ++g) av[0][g] = Dq<DT>::word(word_of(g, 0), zs[g][0], dk);
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
+    for (int st = 0; st < NST; ++st) {
       hook(st);
       const int cur = st & 1, nxt = cur ^ 1;
-      if (st + 1 < 8) {
+      if (st + 1 < NST) {
         const int sn = st + 1;
 #pragma unroll
-        for (int i = 0; i < MT; ++i) bx[nxt][i] = __builtin_bit_cast(V8, xsb[(i * 8 + sn) * 64 + lane]);
+        for (int i = 0; i < MT; ++i) bx[nxt][i] = __builtin_bit_cast(V8, xk[(i * 8 + KW * sn) * 64 + lane]);
 #pragma unroll
-        for (int g = 0; g < 2; ++g) av[nxt][g] = Dq<DT>::word(S.q[g][sn & 1][sn >> 1], zs[g][sn * GPT / 8], dk);
+        for (int g = 0; g < 2; ++g) av[nxt][g] = Dq<DT>::word(word_of(g, sn), zs[g][sn * GPT * KW / 8], dk);
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int g = 0; g < 2; ++g) acc[i][g] = mfma32x32x16(av[cur][g], bx[cur][i], acc[i][g]);
-      if (st + 1 < 8) {
+      if (st + 1 < NST) {
         // 2 MT MFMAs, MT LDS reads and 26 vector operations (two words'
         // dequantisation) per step: after each MFMA one LDS read (while
         // there are any) and up to four vector operations.
@@ -797,7 +825,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       compute(stg[p], xbuf(p), [&](int st) {
 #pragma unroll
-        for (int l = st * kNL / 8; l < (st + 1) * kNL / 8; ++l) {
+        for (int l = st * kNL / NST; l < (st + 1) * kNL / NST; ++l) {
           if (l < XPW) load_x1(pa, kt + NS - 1, l);
           else load_w1(stg[pa], kt + NS - 1, l - XPW);
         }
@@ -827,6 +855,36 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   for (int p = 0; p + 1 < NS; ++p)
     if (i + p < nsteps) step(p, kt0 + i + p);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if constexpr (KW == 2) {
+    // k-wave 1 hands its accumulators to k-wave 0 one column group at a time
+    // through the first stage buffer (64 KiB, [column wave][m32 tile][quad][lane]);
+    // k-wave 0 adds them and stores.
+    f32x4* red = (f32x4*)xs0;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      __syncthreads();  // every wave is done with the stage buffers (or the previous group)
+      if (kw == 1) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            red[((cw * MT + i) * 4 + q) * 64 + lane] =
+                f32x4{acc[i][g][4 * q], acc[i][g][4 * q + 1], acc[i][g][4 * q + 2], acc[i][g][4 * q + 3]};
+      }
+      __syncthreads();
+      if (kw == 0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 v = red[((cw * MT + i) * 4 + q) * 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][g][4 * q + e] += v[e];
+          }
+      }
+    }
+    if (kw == 1) return;
+  }
 
   // Output element e of acc[i][g]: row m0 + 32 i + c32, column 8 (e / 4) + 4 h
   // + e % 4 of group g, i.e. tile slot 2 g + e / 8, column 8 ((e / 4) & 1) +
@@ -881,13 +939,18 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
 // OCC = workgroups per CU the register budget is cut for (2: 256 registers,
 // two waves per SIMD, each workgroup's activation stages in 64 KiB of LDS);
 // NW = waves per workgroup (64 * NW columns).
-template <int BM, int NS, int OCC, int NW, typename DT>
+template <int BM, int NS, int OCC, int NW, typename DT, int KW = 1>
 hipError_t launch_bm32(const TiledArgs& a, int gpt, hipStream_t s) {
   const dim3 grid((unsigned)(a.gx * a.gy * a.ks)), block(64 * NW);
   switch (gpt) {
-    case 1: hipLaunchKernelGGL((mfma32_kernel<BM, 1, NS, OCC, NW, DT>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((mfma32_kernel<BM, 2, NS, OCC, NW, DT>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((mfma32_kernel<BM, 4, 2, OCC, NW, DT>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((mfma32_kernel<BM, 1, NS, OCC, NW, DT, KW>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((mfma32_kernel<BM, 2, NS, OCC, NW, DT, KW>), grid, block, 0, s, a); break;
+    case 4:
+      if constexpr (KW == 1) {
+        hipLaunchKernelGGL((mfma32_kernel<BM, 4, 2, OCC, NW, DT>), grid, block, 0, s, a);
+        break;
+      }
+      return hipErrorInvalidValue;  // four groups per k-tile keep their per-stage zero/scale loads
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -919,6 +982,7 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
     case 4032: return launch_bm32<32, 3, 4, 4, DT>(a, gpt, s);
     case 8064: return launch_bm32<64, 3, 1, 8, DT>(a, gpt, s);
     case 8128: return launch_bm32<128, 3, 1, 8, DT>(a, gpt, s);
+    case 9128: return launch_bm32<128, 3, 1, 8, DT, 2>(a, gpt, s);
     default: return hipErrorInvalidValue;
   }
 }

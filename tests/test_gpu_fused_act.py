@@ -62,7 +62,7 @@ def _check(M, K, I, G=128, dtype=torch.float16, act="silu", with_bias=False, env
     (16, 1024, 9728, "skinny_kernel"),  # wide: two-tile shapes by default
     (40, 2048, 1040, "tiled_kernel"),   # split K
     (300, 1024, 528, "tiled_kernel"),
-    (1024, 2560, 2080, "tiled_kernel"),  # under one round of 128 x 256 tiles: 32x32 kernel, one workgroup per CU
+    (1024, 2560, 2080, "tiled_kernel"),  # over half a round of 128 x 256 tiles: the 8-wave k-wave split
     (512, 1024, 9728, "tiled_kernel"),   # 1.2 rounds of them, 0.6 of 512-column tiles: the 8-wave kernel
 ])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -106,7 +106,7 @@ def test_every_two_tile_decode_shape(variant, M, G, plan):
            kernel="skinny_kernel", plan=plan)
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128])
+@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9128])
 @pytest.mark.parametrize("ks", [1, 3])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 def test_every_prefill_row_block(bm, ks, G, plan):

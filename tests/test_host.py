@@ -242,12 +242,14 @@ def test_plan_overrides_and_plan_info():
     (224, 28672, 4096, 128, 1, 224),     # 64 x 512 tiles would fill 224 CUs: 16x16 128-row block
     (2048, 28672, 4096, 2128, 1, 1792),  # 3.5 rounds: two workgroups per CU
     (2048, 6144, 4096, 8128, 1, 192),    # at most one round of 512-column tiles
-    (2048, 4096, 4096, 128, 1, 256),     # one round of 256-column tiles
+    (2048, 4096, 4096, 9128, 1, 256),    # one round of 256-column tiles: 8 waves splitting the k-steps
     (8192, 28672, 4096, 8128, 1, 3584),  # whole rounds
     (1024, 28672, 4096, 8128, 1, 448),   # last round of 512-column tiles three quarters full
     (2048, 19456, 2560, 2128, 1, 1216),  # last round a quarter full: two workgroups per CU
-    (1024, 6144, 4096, 2128, 1, 192),    # under one round: 32x32 kernel, one workgroup per CU
-    (2048, 2560, 4096, 2128, 1, 160),
+    (1024, 6144, 4096, 9128, 1, 192),    # over half a round, at most one: 32x32 k-wave split
+    (2048, 2560, 4096, 9128, 1, 160),
+    (2048, 2560, 9728, 9128, 1, 160),    # the k-wave split also replaces a 3-way K split
+    (1024, 2560, 4096, 128, 3, 240),     # half a round or less (80 tiles): split K stays
     (512, 19456, 2560, 8128, 1, 152),    # 1.2 rounds of 256-column tiles, 0.6 of 512-column ones
     (64, 2560, 9728, 4032, 11, 220),     # Qwen3-4B down: 32-row blocks up to 112 rows at K <= 12288
     (112, 2560, 9728, 4032, 6, 240),
@@ -268,7 +270,7 @@ def test_tiled_plan_forms_with_fused_activation():
     at prefill sizes (the gated pairs stay within a workgroup in each form)."""
     if ops.device_cu_count() != 256:
         pytest.skip("the forms are pinned for a whole MI355X (256 CUs)")
-    for M, N, K, variant in [(1024, 4160, 2560, 2128), (512, 19456, 1024, 8128), (2048, 19456, 2560, 2128)]:
+    for M, N, K, variant in [(1024, 4160, 2560, 9128), (512, 19456, 1024, 8128), (2048, 19456, 2560, 2128)]:
         assert ops.plan_info(M, N, K, 128, "silu").variant == variant, (M, N, K)
         assert ops.plan_info(M, N, K, 128).variant == variant, (M, N, K)
 
