@@ -442,7 +442,8 @@ def test_every_tiled_variant(bm, G, dtype, plan):
     """Each prefill-kernel instantiation (16x16 MFMA row blocks 32/64/128,
     32x32 MFMA row blocks 64/128 (codes 1064/1128, 2064/2128 and 4032 with
     registers for more workgroups per CU, 8064/8128 with 8 waves and 512
-    columns per workgroup) x groups per 128-row
+    columns per workgroup, 9128 with 8 waves splitting the k-steps of 256
+    columns; with G = 32 the planner keeps its own choice) x groups per 128-row
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
     leave the last row block partial; whole pipeline rounds plus a
