@@ -360,12 +360,12 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
                            env_bm == 2064 || env_bm == 2128 || env_bm == 4032 || env_bm == 8064 || env_bm == 8128 ||
-                           (env_bm == 9128 && g.G >= 64);
+                           ((env_bm == 9064 || env_bm == 9128) && g.G >= 64);
     const int env_ks = knob(kPlanTiledKs, 0);
     const int64_t Np = g.NT * 16;
     double best = 0.0;
     int best_bm = 0, best_ks = 1;
-    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9128}) {
+    for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9064, 9128}) {
       const int bm = code % 1000;
       if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
       if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && !bm32_ok)) continue;
@@ -448,13 +448,20 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // three quarters of the CUs takes the 8-wave 64-row form (two waves per
     // SIMD, less row padding: Llama-3-8B gate_up at M = 160 / 192 69.8 ->
     // 61.5 / 71.1 -> 63.3 us, Qwen3-4B gate_up at M = 224 44.1 -> 39.6 us;
-    // on fuller grids it was 0.5-3% slower), and a 64-row block the two-
-    // workgroup 32x32 form (Qwen3-4B gate_up at M = 128 30.5 -> 28.2 us, 1-8%
-    // faster in every case measured).
+    // on fuller grids it was 0.5-3% slower), and a 64-row block the 32x32
+    // kernel: with at most one round of 64 x 256 tiles its 8-wave k-wave
+    // split (code 9064, two waves per SIMD at one workgroup per CU: Qwen3-4B
+    // gate_up at M = 112 / 128 / 160 / 192 27.8 -> 23.9 / 27.7 -> 23.9 /
+    // 28.4 -> 26.7 / 29.5 -> 27.5 us, Llama-3-8B gate_up at M = 112 / 128
+    // 43.5 -> 41.1 / 43.6 -> 41.8 us, 70B-sized gate_up at M = 40 / 64 83.5 ->
+    // 77.4 / 88.3 -> 80.6 us against the two-workgroup form), else the two-
+    // workgroup form (code 2064: Qwen3-4B gate_up at M = 128 30.5 -> 28.2 us
+    // against the 16x16 kernel, 1-8% faster in every case measured).
     if (!env_bm_ok && ks == 1 && g.G >= 128 && g.M <= 256) {
       const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 63) / 64);
+      const int64_t t64 = ((g.NT + 15) / 16) * ((g.M + 63) / 64);
       if (best_bm == 128 && 4 * t8 <= 3 * (int64_t)g.cus) best_bm = 8064;
-      else if (best_bm == 64) best_bm = 2064;
+      else if (best_bm == 64) best_bm = t64 <= g.cus ? 9064 : 2064;
     }
     p.variant = best_bm;
     p.grid_x = best_bm >= 8000 && best_bm < 9000 ? (g.NT + 31) / 32 : (g.NT + 15) / 16;

@@ -982,6 +982,7 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
     case 4032: return launch_bm32<32, 3, 4, 4, DT>(a, gpt, s);
     case 8064: return launch_bm32<64, 3, 1, 8, DT>(a, gpt, s);
     case 8128: return launch_bm32<128, 3, 1, 8, DT>(a, gpt, s);
+    case 9064: return launch_bm32<64, 3, 1, 8, DT, 2>(a, gpt, s);
     case 9128: return launch_bm32<128, 3, 1, 8, DT, 2>(a, gpt, s);
     default: return hipErrorInvalidValue;
   }

@@ -106,7 +106,7 @@ def test_every_two_tile_decode_shape(variant, M, G, plan):
            kernel="skinny_kernel", plan=plan)
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9128])
+@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9064, 9128])
 @pytest.mark.parametrize("ks", [1, 3])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 def test_every_prefill_row_block(bm, ks, G, plan):

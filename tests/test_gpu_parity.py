@@ -435,7 +435,7 @@ def test_gemv_bf16_and_bias(M):
     assert ok, (err, mx)
 
 
-@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9128])
+@pytest.mark.parametrize("bm", [32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9064, 9128])
 @pytest.mark.parametrize("G", [32, 64, 128, -1])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_every_tiled_variant(bm, G, dtype, plan):

@@ -236,7 +236,8 @@ def test_plan_overrides_and_plan_info():
 @pytest.mark.parametrize("M,N,K,variant,ks,wgs", [
     (8, 4096, 14336, 4032, 16, 256),     # Llama-3-8B down: 32-row 32x32 form, 16 k-slices
     (32, 4096, 14336, 4032, 16, 256),
-    (128, 28672, 4096, 2064, 1, 224),    # Llama-3-8B gate_up: two-workgroup 64-row 32x32 form
+    (128, 28672, 4096, 9064, 1, 224),    # Llama-3-8B gate_up: 64-row 32x32 k-wave split (one round)
+    (64, 57344, 8192, 9064, 1, 224),     # 70B-sized gate_up
     (160, 28672, 4096, 8064, 1, 168),    # 8-wave 64-row form: 168 of 256 CUs
     (256, 19456, 2560, 8064, 1, 152),    # Qwen3-4B gate_up
     (224, 28672, 4096, 128, 1, 224),     # 64 x 512 tiles would fill 224 CUs: 16x16 128-row block
