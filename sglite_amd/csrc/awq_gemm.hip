@@ -416,16 +416,19 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // and 44.6 -> 40.8 us), and one of between one and one and a half rounds
     // the 8-wave kernel when its 512-column tiles fit one round (Qwen3-4B
     // gate_up at M = 512, 304 tiles: 86.0 -> 60.6 us).
-    // Above 256 rows, a grid of more than half and at most one round of
+    // Above 192 rows, a grid of more than half and at most one round of
     // 128 x 256 tiles runs the 32x32-MFMA kernel with 8 waves that split each
     // k-tile's k-steps in two (code 9128: two waves per SIMD on a one-
     // workgroup-per-CU grid, K unsplit): Qwen3-4B down at M = 2048 120.1 (3
     // k-slices) -> 110.5 us, o_proj 60.8 -> 55.2 us; Llama-3-8B o at M = 2048
     // 73.0 -> 70.0 us, qkv at M = 1024 61.4 -> 59.1 us; 70B-sized qkv at
     // M = 512 105.3 -> 98.0 us, o at M = 1024 128.0 -> 124.9 us; Llama-3-8B
-    // down at M = 2048 ties.  On half a round or less the split-K plans win.
+    // down at M = 2048 ties; at 193-256 rows, where every row block pads to
+    // 256, Llama-3-8B / Qwen3-4B gate_up at M = 256 69.0 -> 64.7 / 39.4 ->
+    // 37.3 us (at 192 rows it ties the 64-row forms, which pad less below).
+    // On half a round or less the split-K plans win.
     const int64_t t2_128 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
-    if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 256 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
+    if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 192 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
       best_bm = 9128;
       ks = 1;
     }

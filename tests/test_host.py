@@ -239,8 +239,10 @@ def test_plan_overrides_and_plan_info():
     (128, 28672, 4096, 9064, 1, 224),    # Llama-3-8B gate_up: 64-row 32x32 k-wave split (one round)
     (64, 57344, 8192, 9064, 1, 224),     # 70B-sized gate_up
     (160, 28672, 4096, 8064, 1, 168),    # 8-wave 64-row form: 168 of 256 CUs
-    (256, 19456, 2560, 8064, 1, 152),    # Qwen3-4B gate_up
-    (224, 28672, 4096, 128, 1, 224),     # 64 x 512 tiles would fill 224 CUs: 16x16 128-row block
+    (256, 19456, 2560, 9128, 1, 152),    # Qwen3-4B gate_up: 193-256 rows pad to 256 in every form
+    (192, 19456, 2560, 9064, 1, 228),
+    (224, 28672, 4096, 9128, 1, 224),    # one round of 128 x 256 tiles: the k-wave split
+    (192, 28672, 4096, 8064, 1, 168),
     (2048, 28672, 4096, 2128, 1, 1792),  # 3.5 rounds: two workgroups per CU
     (2048, 6144, 4096, 8128, 1, 192),    # at most one round of 512-column tiles
     (2048, 4096, 4096, 9128, 1, 256),    # one round of 256-column tiles: 8 waves splitting the k-steps
