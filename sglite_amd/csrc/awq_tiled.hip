@@ -545,6 +545,9 @@ hipError_t launch_splitk_reduce(const float* part, const void* bias, void* out, 
 // [m32 tile][k-step][lane] (lane l: row l % 32, columns 8 (l / 32) .. + 7).
 // Each lane's accumulators hold column m = l % 32 of its m32 tile and the
 // output columns 8 j + 4 (l / 32) .. + 3 (j = 0..3) of its column group.
+// With KW = 2 (8 waves, BM x 256), waves w and w + 4 share columns and take
+// the even and odd k-steps of each k-tile, so a one-workgroup-per-CU grid
+// still runs two waves per SIMD without a smaller row block.
 // ---------------------------------------------------------------------------
 
 template <int BM, int GPT, int NS, int OCC, int NW, typename DT, int KW = 1>
@@ -581,7 +584,7 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   constexpr int kNL = XPW + kLoadsW;  // loads per step when spread
   constexpr int kAfterX = (NS - 1) * kLoadsW + (NS - 2) * XPW;
   static_assert(kAfterX < 64, "vector-memory counter range");
-  __shared__ u32x4 xs0[(KW == 2 ? 2 : 1) * XF * 64];  // (KW = 2: also the final exchange, 64 KiB)
+  __shared__ u32x4 xs0[(KW == 2 ? 2 : 1) * XF * 64];  // (KW = 2: also the final exchange, MT * 16 KiB)
   __shared__ u32x4 xs1[XF * 64];
   __shared__ u32x4 xs2[NS > 2 ? XF * 64 : 1];
   __shared__ u32x4 xs3[NS > 3 ? XF * 64 : 1];
@@ -857,8 +860,8 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   if constexpr (KW == 2) {
     // k-wave 1 hands its accumulators to k-wave 0 one column group at a time
-    // through the first stage buffer (64 KiB, [column wave][m32 tile][quad][lane]);
-    // k-wave 0 adds them and stores.
+    // through the first stage buffer (MT * 16 KiB, [column wave][m32 tile][quad]
+    // [lane]); k-wave 0 adds them and stores.
     f32x4* red = (f32x4*)xs0;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
