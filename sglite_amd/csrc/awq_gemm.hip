@@ -427,6 +427,22 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 256, Llama-3-8B / Qwen3-4B gate_up at M = 256 69.0 -> 64.7 / 39.4 ->
     // 37.3 us (at 192 rows it ties the 64-row forms, which pad less below).
     // On half a round or less the split-K plans win.
+    // 65-128 rows on layers the 32-row rule leaves out (wide: more than 8192
+    // columns) with K up to 4096, where the cost model picks 128-row blocks
+    // with split K: K unsplit in the 32-row 32x32 form when its tiles fit one
+    // round (Qwen3-4B gate_up at M = 72 / 80 / 96: 24.6 -> 21.0 / 25.3 ->
+    // 21.2 / 26.5 -> 21.2 us), else in the 64-row k-wave split (Llama-3-8B
+    // gate_up at M = 80 / 96: 41.6 -> 39.6 / 42.8 -> 39.7 us, at 72 a tie).
+    if (!env_bm_ok && best_bm == 128 && g.G >= 128 && g.M > 64 && g.M <= 128 && g.K <= 4096) {
+      const int64_t cb = (g.NT + 15) / 16;
+      if (cb * ((g.M + 31) / 32) <= g.cus) {
+        best_bm = 4032;
+        ks = 1;
+      } else if (cb * ((g.M + 63) / 64) <= g.cus) {
+        best_bm = 9064;
+        ks = 1;
+      }
+    }
     const int64_t t2_128 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
     if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 192 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
       best_bm = 9128;

@@ -231,7 +231,7 @@ def test_qwen3_4b_prefill_sizes(K, N, M):
 
 
 @pytest.mark.parametrize("K,N", LLAMA3_8B)
-@pytest.mark.parametrize("M", [1, 8, 16, 64, 128, 160, 256, 1024, 2048, 8192])
+@pytest.mark.parametrize("M", [1, 8, 16, 64, 96, 128, 160, 256, 1024, 2048, 8192])
 def test_llama3_8b_shapes(K, N, M):
     """Config 2 at every M it names, up to the reference's largest prefill chunk
     (max_extend_tokens = 8192, scheduler/config.py:20), and the decode batches
