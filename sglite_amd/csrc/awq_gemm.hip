@@ -349,13 +349,16 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 4032 = the same at 32 rows with registers for four;
     // 8064, 8128 = 8 waves and 512 columns per workgroup, one per CU.
     // 32-row blocks beyond 32 rows, up to 160, on layers of at most 8192
-    // columns and 8192 rows of K (graph-replay A/B at M = 48..160 over the
+    // columns and 4096 rows of K (graph-replay A/B at M = 48..160 over the
     // Llama-3-8B and Qwen3-4B linears: qkv and o 7-19% faster in the 32x32
     // kernel with four workgroups per CU; wider or deeper layers, gate_up and
     // down, 3-16% slower, so they keep 64- and 128-row blocks), and up to 112
     // rows on layers of at most 4096 columns and 12288 rows of K (Qwen3-4B
-    // down at M = 40..112: 5-10% faster; even at 128, slower at 160).
-    const bool bm32_ok = g.M <= 32 || (g.M <= 160 && g.N <= 8192 && g.K <= 8192) ||
+    // down at M = 40..112: 5-10% faster; even at 128, slower at 160).  With
+    // K of 4097-8192 the 64-row block stays (a 70B-sized o_proj, K = N = 8192,
+    // at M = 40 / 64 / 96 / 128: 21.6 -> 20.5 / 23.4 -> 22.4 / 33.9 -> 29.9 /
+    // 35.9 -> 31.2 us against 32-row blocks).
+    const bool bm32_ok = g.M <= 32 || (g.M <= 160 && g.N <= 8192 && g.K <= 4096) ||
                          (g.M <= 112 && g.N <= 4096 && g.K <= 12288);
     const int env_bm = knob(kPlanTiledBm, 0);
     const bool env_bm_ok = env_bm == 32 || env_bm == 64 || env_bm == 128 || env_bm == 1064 || env_bm == 1128 ||
