@@ -446,6 +446,22 @@ GemmPlan plan_gemm(const Geom& g, int act) {
         ks = 1;
       }
     }
+    // 129-192 rows where the cost model picks 128-row blocks with split K:
+    // the 64-row k-wave split with the most k-slices (up to the chosen count)
+    // whose grid fits one round (Llama-3-8B down at M = 160 / 192: 39.9 ->
+    // 36.3 / 40.7 -> 37.7 us with 4 slices; 70B-sized o at M = 160 / 192:
+    // 44.6 -> 40.9 / 45.2 -> 42.6 us and down 120.1 -> 115.1 / 121.3 -> 119.2
+    // us with 2 slices).
+    if (!env_bm_ok && best_bm == 128 && ks > 1 && g.G >= 128 && g.M > 128 && g.M <= 192) {
+      const int64_t t64 = ((g.NT + 15) / 16) * ((g.M + 63) / 64);
+      int64_t k9 = 0;
+      for (int c : {2, 3, 4, 6, 8, 12, 16})
+        if (c <= ks && t64 * c <= g.cus) k9 = c;
+      if (k9 >= 2) {
+        best_bm = 9064;
+        ks = k9;
+      }
+    }
     const int64_t t2_128 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
     if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 192 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
       best_bm = 9128;

@@ -240,6 +240,8 @@ def test_plan_overrides_and_plan_info():
     (64, 57344, 8192, 9064, 1, 224),     # 70B-sized gate_up
     (96, 19456, 2560, 4032, 1, 228),     # wide, 65-128 rows, K <= 4096: K unsplit in 32-row blocks
     (96, 28672, 4096, 9064, 1, 224),     # ... or in the 64-row k-wave split when 32-row tiles overflow
+    (160, 4096, 14336, 9064, 4, 192),    # 129-192 rows, split K: the 64-row k-wave split, one round
+    (192, 8192, 8192, 9064, 2, 192),
     (160, 28672, 4096, 8064, 1, 168),    # 8-wave 64-row form: 168 of 256 CUs
     (256, 19456, 2560, 9128, 1, 152),    # Qwen3-4B gate_up: 193-256 rows pad to 256 in every form
     (192, 19456, 2560, 9064, 1, 228),
