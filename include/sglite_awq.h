@@ -47,8 +47,21 @@ enum { AWQ_DTYPE_FP16 = 0, AWQ_DTYPE_BF16 = 1 };
 /* Message of the last failed call on this thread ("" if none). */
 const char* awq_last_error(void);
 
-/* Library version string, e.g. "sglite-awq-gfx950 0.1". */
+/* Library version string, e.g. "sglite-awq-gfx950 0.3". */
 const char* awq_version(void);
+
+/* ABI revision of this header.  A caller checks awq_abi_version() ==
+ * AWQ_ABI_VERSION (the value it was built against) before its first call:
+ *   1  the first release;
+ *   2  awq_w4a16_gemm / awq_w4a16_gemm_act take `int64_t counter_bytes`
+ *      after `counters` (the symbol names did not change);
+ *   3  awq_counter_bytes(N) covers the tiled kernels' split-tile counters
+ *      too (AWQ_COUNTER_TILE_BYTES ahead of the per-column-tile counters),
+ *      counters must be 128-byte aligned; awq_noalloc_init and the planner
+ *      knobs AWQ_PLAN_TILED_FIXUP / AWQ_PLAN_FIXUP_POLLS are new.
+ * No counterpart in the reference (its kernels are Python and Triton). */
+#define AWQ_ABI_VERSION 3
+int awq_abi_version(void);
 
 /* ---- post-load repack ------------------------------------------------------
  * Replaces the Marlin post-load step of
@@ -103,11 +116,20 @@ int awq_dequant_repacked(const void* w, const void* s, const void* z, int dtype,
  *
  * Split-K scratch: `ws` must hold awq_workspace_bytes(M, N, K, G) bytes (any
  * content; may be NULL when that is 0).  `counters` (int32, counter_bytes
- * long) must hold at least awq_counter_bytes(N) bytes that are zero before the
- * first call on them; every call leaves them zero again.  Both are checked
- * whenever the plan splits K (AWQ_STATUS_WORKSPACE if missing or short).
- * Calls sharing `counters` must not run concurrently (use one counters
- * buffer per stream). */
+ * long, 128-byte aligned) must hold at least awq_counter_bytes(N) bytes that
+ * are zero before the first call on them; every call leaves them valid for
+ * the next (the decode kernels' per-column-tile counters zero again, the
+ * tiled kernels' split-tile counters advanced consistently), whatever shape
+ * the next call has.  A buffer sized for the largest N may be shared by
+ * every linear of a stream.  Both are checked whenever the plan splits K
+ * (AWQ_STATUS_WORKSPACE if missing or short); the tiled kernels (kind 1)
+ * accept NULL counters and then sum their k-slices in a second kernel
+ * instead of in the GEMM kernel itself.  Calls sharing `counters` must not run
+ * concurrently (use one counters buffer per stream).
+ * Layout: AWQ_COUNTER_TILE_BYTES of split-tile counters (32 words per output
+ * tile of a split tiled plan, at most 512 tiles), then one int32 per
+ * 16-column tile. */
+#define AWQ_COUNTER_TILE_BYTES (64ll << 10)
 int64_t awq_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t G);
 /* Which kernel awq_w4a16_gemm runs for this shape: 0 = decode split-K kernel,
  * 1 = tiled MFMA kernel, 2 = small-batch GEMV kernel, 3 = k-slice decode
@@ -133,6 +155,12 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
  * No counterpart in the reference. */
 #define AWQ_NOALLOC_WORKSPACE_BYTES (64ll << 20)
 #define AWQ_NOALLOC_MAX_N (1ll << 20)
+/* Resolve the current device's scratch and clear its counters on `stream`
+ * (a fill kernel, no allocation).  Optional: the first awq_w4a16_gemm_noalloc
+ * call on a device does the same, and if that call is being captured into a
+ * graph the fill kernel becomes a node of the graph.  Call it once per device
+ * before capturing to keep the graph free of it. */
+int awq_noalloc_init(awq_stream_t stream);
 int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
                            int64_t M, int64_t N, int64_t K, int64_t G, int dtype, awq_stream_t stream);
 
@@ -173,10 +201,18 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
  *                            kernel); 1064, 1128, 2064, 2128, 4032 (32x32x16
  *                            MFMA kernel at 64/128/32 rows with registers for
  *                            1, 2 or 4 workgroups per CU); 8064, 8128 (its
- *                            8-wave, 512-column form)
+ *                            8-wave, 512-column form); 9064, 9128 (its 8-wave
+ *                            k-wave-split form at 64/128 rows, only with
+ *                            G >= 64)
  *   AWQ_PLAN_TILED_KS        tiled k-slices
  *   AWQ_PLAN_KSLICE_VARIANT  k-slice decode-kernel shape wn*100 + wk*10 + kpw
- *                            (M <= 32; any other value leaves the plan alone) */
+ *                            (M <= 32; any other value leaves the plan alone)
+ *   AWQ_PLAN_TILED_FIXUP     0: split-K tiled plans sum their k-slices in a
+ *                            second kernel (default: inside the GEMM kernel,
+ *                            when the counters are given)
+ *   AWQ_PLAN_FIXUP_POLLS     how often a k-slice workgroup polls for its
+ *                            tile's other slices before it leaves the sum to
+ *                            the last one (0: never waits) */
 enum {
   AWQ_PLAN_GEMV_MAX_M = 0,
   AWQ_PLAN_GEMV_VARIANT = 1,
@@ -186,7 +222,9 @@ enum {
   AWQ_PLAN_TILED_MIN_M = 5,
   AWQ_PLAN_TILED_BM = 6,
   AWQ_PLAN_TILED_KS = 7,
-  AWQ_PLAN_KSLICE_VARIANT = 8
+  AWQ_PLAN_KSLICE_VARIANT = 8,
+  AWQ_PLAN_TILED_FIXUP = 9,
+  AWQ_PLAN_FIXUP_POLLS = 10
 };
 int awq_set_plan_override(int knob, int value);
 void awq_clear_plan_overrides(void);
@@ -211,6 +249,9 @@ int awq_device_cu_count(void);
  * launch of that shape can reach at all (the decode roofline's attainable
  * ceiling). */
 int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activation, int64_t* info);
+/* 1 if that plan splits K on the tiled kernels and sums the k-slices inside
+ * the GEMM kernel (when awq_w4a16_gemm is given counters), 0 otherwise. */
+int awq_gemm_plan_fixup(int64_t M, int64_t N, int64_t K, int64_t G, int activation);
 int awq_stream_probe(const void* src, int64_t bytes, int64_t grid, int block, uint32_t* sink, int64_t sink_bytes,
                      awq_stream_t stream);
 /* awq_mfma_probe: `grid` workgroups of `block` threads (64..256), each wave

@@ -31,6 +31,7 @@ _int = ctypes.c_int
 SIGNATURES = {
     "awq_last_error": (ctypes.c_char_p, []),
     "awq_version": (ctypes.c_char_p, []),
+    "awq_abi_version": (_int, []),
     "awq_repacked_weight_bytes": (_i64, [_i64, _i64]),
     "awq_repacked_scale_bytes": (_i64, [_i64, _i64, _i64]),
     "awq_repacked_zero_bytes": (_i64, [_i64, _i64, _i64]),
@@ -43,6 +44,7 @@ SIGNATURES = {
     "awq_gemm_kernel_kind": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64,
                               _vp]),
+    "awq_noalloc_init": (_int, [_vp]),
     "awq_w4a16_gemm_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "awq_workspace_bytes_act": (_i64, [_i64, _i64, _i64, _i64]),
     "awq_gemm_kernel_kind_act": (_int, [_i64, _i64, _i64, _i64]),
@@ -52,6 +54,7 @@ SIGNATURES = {
     "awq_clear_plan_overrides": (None, []),
     "awq_device_cu_count": (_int, []),
     "awq_gemm_plan_info": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_i64)]),
+    "awq_gemm_plan_fixup": (_int, [_i64, _i64, _i64, _i64, _int]),
     "awq_stream_probe": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _vp]),
     "awq_mfma_probe": (_int, [_i64, _i64, _int, _vp, _i64, _vp]),
     "awq_moe_expert_strides": (_int, [_i64, _i64, _i64, ctypes.POINTER(_i64), ctypes.POINTER(_i64),
@@ -77,6 +80,13 @@ AWQ_PLAN_TILED_MIN_M = 5
 AWQ_PLAN_TILED_BM = 6
 AWQ_PLAN_TILED_KS = 7
 AWQ_PLAN_KSLICE_VARIANT = 8
+AWQ_PLAN_TILED_FIXUP = 9
+AWQ_PLAN_FIXUP_POLLS = 10
+
+# The header revision this binding follows (AWQ_ABI_VERSION).
+AWQ_ABI_VERSION = 3
+# Split-tile counters ahead of the per-column-tile counters (AWQ_COUNTER_TILE_BYTES).
+AWQ_COUNTER_TILE_BYTES = 64 << 10
 
 AWQ_NOALLOC_WORKSPACE_BYTES = 64 << 20
 AWQ_NOALLOC_MAX_N = 1 << 20
@@ -103,6 +113,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             "(run __graft_entry__.build() or `make -C sglite_amd/csrc`)."
         )
     lib = ctypes.CDLL(path)
+    # A library built from another header revision would take these
+    # argument lists differently: refuse it before binding anything.
+    abi = getattr(lib, "awq_abi_version", None)
+    found = abi() if abi is not None else 1
+    if found != AWQ_ABI_VERSION:
+        raise RuntimeError(f"{path} implements AWQ ABI {found}, this binding needs {AWQ_ABI_VERSION}: rebuild it")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

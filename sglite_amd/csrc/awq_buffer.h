@@ -8,9 +8,16 @@ namespace sgl_awq {
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, dword data format (gfx9)
 // Buffer cache policy SC1 (device scope): the bits the compiler gives an
-// agent-scope atomic load or store, so such an access is coherent across the
-// XCDs' L2 caches once it has completed.
+// agent-scope atomic store; a store with it is written through to memory
+// and has reached it once the store has completed (vmcnt).
 constexpr int kCacheDevice = 16;
+// Buffer cache policy SC0 | SC1 | NT for loads of data that other
+// workgroups (possibly on other XCDs) wrote in the same launch: the
+// system-scope bits, which miss in every cache level of the reading CU and
+// XCD, plus the streaming hint.  Loads with SC1 alone were measured to return
+// a stale copy in that situation on MI355X (an in-kernel split-K sum read
+// the previous launch's partials); SC0 | SC1 did not.
+constexpr int kCacheCoherentLoad = 19;
 // Buffer cache policy NT (non-temporal): a stream read once.
 constexpr int kCacheStream = 2;
 

@@ -16,6 +16,7 @@
 
 #include "../../include/sglite_awq.h"
 #include "awq_epilogue.h"
+#include "awq_fixup.h"
 #include "awq_launch.h"
 
 using namespace sgl_awq;
@@ -73,17 +74,25 @@ int check_shape(int64_t K, int64_t N, int64_t G, int dtype, int64_t* G_out) {
   return AWQ_STATUS_OK;
 }
 
-// Split-K arrival counters: the GEMV and decode kernels index one int32 per
-// column tile (awq_counter_bytes); the tiled kernel reduces in a second
-// kernel and needs none.
+// Split-K counters (awq_counter_bytes): the split tiles' counters of the
+// tiled kernels' in-kernel reduction (kFixupBytes), then one int32 per column
+// tile for the GEMV and decode kernels.  The tiled kernels take them when
+// given (else a second kernel sums the k-slices); the others need them.
+constexpr int64_t counter_bytes_for(int64_t N) { return kFixupBytes + ((N + 15) / 16) * 4; }
+static_assert(AWQ_COUNTER_TILE_BYTES == kFixupBytes, "header and kernels agree on the tile counters");
+
 int check_counters(const GemmPlan& p, int64_t N, const int32_t* counters, int64_t counter_bytes, const char* who) {
-  if (p.kind == 1) return AWQ_STATUS_OK;
-  const int64_t need = ((N + 15) / 16) * 4;
+  if (p.kind == 1) {
+    if (counters && !aligned(counters, 128))
+      return fail(AWQ_STATUS_WORKSPACE, "%s: counters must be 128-byte aligned", who);
+    return AWQ_STATUS_OK;
+  }
+  const int64_t need = counter_bytes_for(N);
   if (!counters) return fail(AWQ_STATUS_WORKSPACE, "%s: split-K needs the counters buffer", who);
   if (counter_bytes < need)
     return fail(AWQ_STATUS_WORKSPACE, "%s: counters of %lld bytes needed, %lld given", who, (long long)need,
                 (long long)counter_bytes);
-  if (!aligned(counters, 4)) return fail(AWQ_STATUS_WORKSPACE, "%s: counters must be 4-byte aligned", who);
+  if (!aligned(counters, 128)) return fail(AWQ_STATUS_WORKSPACE, "%s: counters must be 128-byte aligned", who);
   return AWQ_STATUS_OK;
 }
 
@@ -109,14 +118,17 @@ int gemm_prepare(const void* x, const void* w, const void* s, const void* z, con
 }
 
 // ---- static scratch of awq_w4a16_gemm_noalloc ------------------------------
-// The split-K workspace (kScratchWsBytes) followed by the arrival counters
-// (kScratchCounterBytes), in device memory that exists from the code
-// object's load to the end of the process, one copy per device.  In host
-// code `scratch` names a host-side stand-in, never the device memory: the
-// device address comes from hipGetSymbolAddress, once per device, and only
-// that address is handed to kernels.
-constexpr int64_t kScratchWsBytes = int64_t(64) << 20;
-constexpr int64_t kScratchCounterBytes = int64_t(256) << 10;
+// The split-K workspace (kScratchWsBytes) followed by the counters
+// (kScratchCounterBytes: the split tiles' counters, then one int32 per column
+// tile for up to AWQ_NOALLOC_MAX_N columns), in device memory that exists
+// from the code object's load to the end of the process, one copy per
+// device.  In host code `scratch` names a host-side stand-in, never the device
+// memory: the device address comes from hipGetSymbolAddress, once per device,
+// and only that address is handed to kernels.
+constexpr int64_t kScratchWsBytes = AWQ_NOALLOC_WORKSPACE_BYTES;
+constexpr int64_t kScratchCounterBytes = kFixupBytes + AWQ_NOALLOC_MAX_N / 16 * 4;
+static_assert(kScratchWsBytes % 256 == 0, "the counters start 256-byte aligned");
+static_assert(kScratchCounterBytes == counter_bytes_for(AWQ_NOALLOC_MAX_N), "scratch counters cover AWQ_NOALLOC_MAX_N columns");
 static __device__ __align__(256) unsigned char scratch[kScratchWsBytes + kScratchCounterBytes];
 
 constexpr int kScratchDevices = 64;
@@ -129,9 +141,12 @@ __global__ void zero_words_kernel(uint32_t* p, int64_t n) {
 }
 
 // Device address of the current device's scratch.  The first call on a device
-// resolves it and, unless `stream` is being captured into a graph, clears the
-// counters on `stream` with a fill kernel (they also start zeroed from the
-// code object's zero-filled data; every GEMM leaves them zero again).
+// resolves it and clears the counters on `stream` with a fill kernel (they
+// also start zeroed from the code object's zero-filled data); when `stream`
+// is being captured into a graph the fill kernel becomes a node of the graph
+// and runs ahead of the GEMM at every replay.  Every GEMM leaves the counters
+// in a valid state for the next (awq_fixup.h; the decode kernels' are left
+// zero).  awq_noalloc_init does the same ahead of any capture.
 int scratch_base(hipStream_t stream, char** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "hipGetDevice failed");
@@ -144,16 +159,11 @@ int scratch_base(hipStream_t stream, char** out) {
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr)
       return fail(AWQ_STATUS_HIP_ERROR, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cap) != hipSuccess)
-      return fail(AWQ_STATUS_HIP_ERROR, "hipStreamIsCapturing failed");
-    if (cap == hipStreamCaptureStatusNone) {
-      const int64_t n = kScratchCounterBytes / 4;
-      hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                         (uint32_t*)((char*)ptr + kScratchWsBytes), n);
-      const hipError_t le = hipGetLastError();
-      if (le != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "scratch clear launch: %s", hipGetErrorString(le));
-    }
+    const int64_t n = kScratchCounterBytes / 4;
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       (uint32_t*)((char*)ptr + kScratchWsBytes), n);
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "scratch clear launch: %s", hipGetErrorString(le));
     g_scratch_ptr[dev] = (char*)ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -178,7 +188,9 @@ extern "C" {
 
 const char* awq_last_error(void) { return g_last_error.c_str(); }
 
-const char* awq_version(void) { return "sglite-awq-gfx950 0.1"; }
+const char* awq_version(void) { return "sglite-awq-gfx950 0.3"; }
+
+int awq_abi_version(void) { return AWQ_ABI_VERSION; }
 
 int64_t awq_repacked_weight_bytes(int64_t K, int64_t N) {
   if (K <= 0 || N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "K and N must be positive");
@@ -277,7 +289,7 @@ int awq_gemm_kernel_kind(int64_t M, int64_t N, int64_t K, int64_t G) {
 
 int64_t awq_counter_bytes(int64_t N) {
   if (N <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "N must be positive");
-  return ((N + 15) / 16) * 4;
+  return counter_bytes_for(N);
 }
 
 int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
@@ -296,8 +308,16 @@ int awq_w4a16_gemm(const void* x, const void* w, const void* s, const void* z, c
     st = check_counters(p, N, counters, counter_bytes, "awq_w4a16_gemm");
     if (st != 0) return st;
   }
-  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, counters ? counter_bytes : 0,
+                                kActNone, (hipStream_t)stream),
                     "awq_w4a16_gemm launch");
+}
+
+int awq_noalloc_init(awq_stream_t stream) {
+  const TraceRange range("awq_noalloc_init");
+  char* base = nullptr;
+  const int st = scratch_base((hipStream_t)stream, &base);
+  return st != 0 ? st : ok();
 }
 
 int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const void* z, const void* bias, void* out,
@@ -315,16 +335,17 @@ int awq_w4a16_gemm_noalloc(const void* x, const void* w, const void* s, const vo
                   "awq_w4a16_gemm_noalloc: this shape's split-K workspace (%lld bytes) exceeds the static scratch "
                   "of %lld bytes; use awq_w4a16_gemm with a caller workspace",
                   (long long)p.ws_bytes, (long long)kScratchWsBytes);
-    if (p.kind != 1 && (N + 15) / 16 * 4 > kScratchCounterBytes)
+    if (p.kind != 1 && N > AWQ_NOALLOC_MAX_N)
       return fail(AWQ_STATUS_UNSUPPORTED, "awq_w4a16_gemm_noalloc: N = %lld exceeds the static counters' %lld columns",
-                  (long long)N, (long long)(kScratchCounterBytes / 4 * 16));
+                  (long long)N, (long long)AWQ_NOALLOC_MAX_N);
     char* base = nullptr;
     st = scratch_base((hipStream_t)stream, &base);
     if (st != 0) return st;
     ws = base;
     counters = (int32_t*)(base + kScratchWsBytes);
   }
-  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, kActNone, (hipStream_t)stream),
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters,
+                                counters ? kScratchCounterBytes : 0, kActNone, (hipStream_t)stream),
                     "awq_w4a16_gemm_noalloc launch");
 }
 
@@ -385,7 +406,8 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
     const int st2 = check_counters(p, N, counters, counter_bytes, "awq_w4a16_gemm_act");
     if (st2 != 0) return st2;
   }
-  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, act, (hipStream_t)stream),
+  return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, counters ? counter_bytes : 0, act,
+                                (hipStream_t)stream),
                     "awq_w4a16_gemm_act launch");
 }
 
@@ -417,6 +439,17 @@ int awq_gemm_plan_info(int64_t M, int64_t N, int64_t K, int64_t G, int activatio
   info[4] = plan_threads(p);
   info[5] = p.ws_bytes;
   return ok();
+}
+
+int awq_gemm_plan_fixup(int64_t M, int64_t N, int64_t K, int64_t G, int activation) {
+  int64_t Gr = 0;
+  const int st = check_shape(K, N, G, AWQ_DTYPE_FP16, &Gr);
+  if (st != 0) return st;
+  if (M <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_gemm_plan_fixup: M must be positive");
+  if (activation != 0 && activation != AWQ_ACT_SILU && activation != AWQ_ACT_GELU)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "awq_gemm_plan_fixup: unknown activation %d", activation);
+  const GemmPlan p = plan_gemm(make_geom(M, N, K, Gr), activation == 0 ? kActNone : kActSilu);
+  return p.kind == 1 && p.ks > 1 && p.fixup ? 1 : 0;
 }
 
 int awq_mfma_probe(int64_t iters, int64_t grid, int block, float* sink, int64_t sink_bytes, awq_stream_t stream) {

@@ -22,6 +22,7 @@
 
 #include "awq_device.h"
 #include "awq_epilogue.h"
+#include "awq_fixup.h"
 #include "awq_launch.h"
 
 namespace sgl_awq {
@@ -34,7 +35,8 @@ namespace {
 // Planner overrides (tests and sweeps only; see awq_set_plan_override).  An
 // unset knob holds kUnset and the planner's own choice stands.
 constexpr int kUnset = INT_MIN;
-std::atomic<int> g_override[kPlanKnobs] = {kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset, kUnset};
+std::atomic<int> g_override[kPlanKnobs] = {kUnset, kUnset, kUnset, kUnset, kUnset, kUnset,
+                                           kUnset, kUnset, kUnset, kUnset, kUnset};
 
 int knob(int k, int dflt) {
   const int v = g_override[k].load(std::memory_order_relaxed);
@@ -507,6 +509,18 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     p.ktc = (int)((g.KT + ks - 1) / ks);
     p.ks = (int)((g.KT + p.ktc - 1) / p.ktc);  // every slice gets >= 1 k-tile
     p.ws_bytes = p.ks > 1 ? (int64_t)p.ks * g.M * g.NT * 16 * 4 : 0;
+    // On request (AWQ_PLAN_TILED_FIXUP) the k-slice workgroups sum the slices
+    // themselves (awq_fixup.h) when the tiles fit the counters and the grid
+    // fits one workgroup per CU, so that on an idle device every k-slice of a
+    // tile is resident together.  Off by default: graph-replay A/B over the
+    // Qwen3-4B and Llama-3-8B split-K shapes at M = 16..256 measured the second
+    // kernel 3-14% faster at M <= 160 (Qwen3-4B gate_up at M = 32: 15.5 against
+    // 17.2 us; Llama-3-8B down at M = 16: 14.0 against 16.0 us), equal at 128
+    // and 6% slower only for the Llama-3-8B o_proj at M = 256.
+    const int64_t tiles = p.grid_x * p.grid_y;
+    p.fixup = p.ks > 1 && p.ks <= kFixupMaxSlices && tiles <= kFixupMaxTiles && tiles * p.ks <= g.cus &&
+              knob(kPlanTiledFixup, 0) != 0;
+    p.polls = std::max(0, knob(kPlanFixupPolls, kFixupDefaultPolls));
   }
   return p;
 }
@@ -519,12 +533,14 @@ int plan_threads(const GemmPlan& p) {
 }
 
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
-                       hipStream_t s) {
-  if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
-  if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
-  if (p.kind == 3) return launch_kslice(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
-  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, counters, act, s);
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       int64_t counter_bytes, int act, hipStream_t s) {
+  // The decode kernels' per-column-tile counters follow the split tiles' ones.
+  int32_t* col = counters != nullptr && counter_bytes >= kFixupBytes ? counters + kFixupBytes / 4 : nullptr;
+  if (p.kind == 0) return launch_skinny(p, x, w, sr, zr, bias, out, dtype, g, ws, col, act, s);
+  if (p.kind == 2) return launch_gemv(p, x, w, sr, zr, bias, out, dtype, g, ws, col, act, s);
+  if (p.kind == 3) return launch_kslice(p, x, w, sr, zr, bias, out, dtype, g, ws, col, act, s);
+  return launch_tiled(p, x, w, sr, zr, bias, out, dtype, g, ws, col != nullptr ? counters : nullptr, act, s);
 }
 
 }  // namespace sgl_awq

@@ -20,13 +20,14 @@
 // activation rows below M are loaded; k-chunks past K read as zeros.
 //
 // Split-K handoff: each workgroup writes its fp32 partial with device-scope
-// (SC1) 16-byte stores and waits until they have completed; one thread then
-// increments the column group's arrival counter (a device-scope atomic).  The
-// workgroup that sees the count reach ks - 1 reads the ks partials back with
-// device-scope loads, adds them in slice order -- the same order whichever
-// workgroup finishes last, so results are deterministic -- stores the output
-// (bias, fused gate/up activation) and resets the counter for the next
-// launch.  Every access that crosses workgroups is a device-scope one, so no
+// (SC1, write-through) 16-byte stores and waits until they have completed;
+// one thread then increments the column group's arrival counter (a
+// device-scope atomic).  The workgroup that sees the count reach ks - 1 reads
+// the ks partials back with system-scope loads (kCacheCoherentLoad), adds
+// them in slice order -- the same order whichever workgroup finishes last, so
+// results are deterministic -- stores the output (bias, fused gate/up
+// activation) and resets the counter for the next launch.  Every access that
+// crosses workgroups bypasses the caches it could find stale, so no
 // cache-wide writeback or invalidate is executed.
 //
 // Workgroup ids map XCD-aware onto (column group, k-slice): the workgroups one
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(256, 2) void kslice_kernel(KsArgs a) {
     for (int i = 0; i < 16; ++i)
       if (i < ks)
         v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off + (uint32_t)i * slice, 0,
-                                                                               kCacheDevice));
+                                                                               kCacheCoherentLoad));
     f32x4 tot = v[0];
 #pragma unroll
     for (int i = 1; i < 16; ++i)

@@ -29,7 +29,9 @@ enum : int {
   kPlanTiledBm = 6,       // tiled row block (32, 64, 128)
   kPlanTiledKs = 7,       // tiled k-slices
   kPlanKsliceVariant = 8, // in-kernel split-K decode kernel shape wn*100 + wk*10 + kpw
-  kPlanKnobs = 9
+  kPlanTiledFixup = 9,    // 0: tiled split-K plans sum their slices in a second kernel
+  kPlanFixupPolls = 10,   // poll bound of the in-kernel split-K reduction (0: only the last arrival reduces)
+  kPlanKnobs = 11
 };
 bool set_plan_override(int knob, int value);
 void clear_plan_overrides();
@@ -54,6 +56,8 @@ struct GemmPlan {
   int64_t grid_x, grid_y;
   int64_t ws_bytes;
   int64_t lds_bytes;  // dynamic LDS (GEMV)
+  int fixup;          // tiled split K: the k-slice workgroups sum the slices (awq_fixup.h)
+  int polls;          // ... each polling at most this often for the tile's other slices
 };
 
 // act: fused gate/up activation of the output (0 none, 1 silu, 2 gelu; the
@@ -74,9 +78,12 @@ int64_t tiled_max_k(int bm);
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
                         const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
                         hipStream_t s);
+// `counters`: the caller's counters buffer (awq_counter_bytes: the split
+// tiles' counters of the tiled kernels, then one int32 per column tile for
+// the decode kernels) of `counter_bytes` bytes, or null.
 hipError_t launch_gemm(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters, int act,
-                       hipStream_t s);
+                       const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
+                       int64_t counter_bytes, int act, hipStream_t s);
 
 // Grouped MoE path (awq_moe.hip).
 // Byte strides between consecutive experts' repacked weights, scales, zeros.

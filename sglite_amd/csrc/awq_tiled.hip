@@ -42,6 +42,7 @@
 #include "awq_buffer.h"
 #include "awq_device.h"
 #include "awq_epilogue.h"
+#include "awq_fixup.h"
 #include "awq_launch.h"
 
 namespace sgl_awq {
@@ -60,6 +61,8 @@ struct TiledArgs {
   int gx, gy;  // column blocks (256 columns), row blocks (BM rows)
   int ks, ktc;  // k-slices and k-tiles per slice
   int act;      // fused gate/up activation (kActNone: plain GEMM)
+  uint32_t* tcnt;  // split tiles' counters for the in-kernel reduction (null: a second kernel sums the slices)
+  int polls;       // poll bound of a workgroup waiting for its tile's other k-slices
 };
 
 // Workgroup id -> (column block, row block).  Ids b, b + 8, b + 16, ... run
@@ -447,12 +450,16 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     return;
   }
 
-  // Split K: this slice's partial tile, in fp32, for the reduction kernel.
-  // Written through to memory (device-scope stores): no dirty L2 lines are
-  // left for the end-of-kernel writeback that the reduction kernel waits for.
-  // The planner keeps ks * M * Np * 4 below 2^31, so one slice's byte
-  // offsets fit the 32-bit buffer offset.
+  // Split K: this slice's partial tile, in fp32, written through to memory
+  // (device-scope stores), then summed by the tile's k-slice workgroups
+  // (splitk_fixup) or by the reduction kernel: no dirty L2 lines are left for
+  // the end-of-kernel writeback that the reduction kernel waits for.  The
+  // planner keeps ks * M * Np * 4 below 2^31, so one slice's byte offsets fit
+  // the 32-bit buffer offset.
   const int Np = a.NT * 16;
+  uint32_t* tc = a.tcnt != nullptr ? a.tcnt + (by * a.gx + bx) * kFixupWords : nullptr;
+  uint32_t fbase = 0;
+  if (tc != nullptr && threadIdx.x == 0) fbase = ld_sys_u32(tc + 1);
   const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part + (int64_t)kslice * a.M * Np, (uint32_t)a.M * (uint32_t)Np * 4u);
 #pragma unroll
   for (int mt = 0; mt < MTL; ++mt)
@@ -465,6 +472,12 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
                                                ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
                                                kCacheDevice);
     }
+  if (tc != nullptr) {
+    // 256 columns (16 tiles) per workgroup; with a fused activation 128 gate columns.
+    const FixupTile<DT> ft{a.part, out, bias, a.M, a.N, Np, a.ks, a.act, m0, rows,
+                           a.act ? bx * 128 : bx * 256, a.act ? 32 : 64};
+    splitk_fixup<256, DT>(ft, tc, fbase, kslice, a.polls);
+  }
 }
 
 // Sum of the k-slices' partials in slice order (deterministic), plus bias, in
@@ -886,7 +899,9 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
           }
       }
     }
-    if (kw == 1) return;
+    // k-wave 1 has nothing left to store; with the in-kernel reduction it
+    // still helps to sum the tile's k-slices.
+    if (kw == 1 && (a.ks == 1 || a.tcnt == nullptr)) return;
   }
 
   // Output element e of acc[i][g]: row m0 + 32 i + c32, column 8 (e / 4) + 4 h
@@ -922,21 +937,32 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     return;
   }
   const int Np = a.NT * 16;
+  uint32_t* tc = a.tcnt != nullptr ? a.tcnt + (by * a.gx + bx) * kFixupWords : nullptr;
+  uint32_t fbase = 0;
+  if (tc != nullptr && threadIdx.x == 0) fbase = ld_sys_u32(tc + 1);
   const __amdgpu_buffer_rsrc_t pr = make_rsrc(a.part + (int64_t)kslice * a.M * Np, (uint32_t)a.M * (uint32_t)Np * 4u);
+  if (KW == 1 || kw == 0) {
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+      for (int g = 0; g < 2; ++g)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = i * 32 + c32;
-        const int slot = 2 * g + (j >> 1);
-        const int n0 = pt[slot] * 16 + 8 * (j & 1) + 4 * h;
-        if (m < rows && pv[slot])
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, quad(acc[i][g], j)), pr,
-                                                 ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
-                                                 kCacheDevice);
-      }
+        for (int j = 0; j < 4; ++j) {
+          const int m = i * 32 + c32;
+          const int slot = 2 * g + (j >> 1);
+          const int n0 = pt[slot] * 16 + 8 * (j & 1) + 4 * h;
+          if (m < rows && pv[slot])
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, quad(acc[i][g], j)), pr,
+                                                   ((uint32_t)(m0 + m) * (uint32_t)Np + (uint32_t)n0) * 4u, 0,
+                                                   kCacheDevice);
+        }
+  }
+  if (tc != nullptr) {
+    // 64 CW columns (4 CW tiles) per workgroup; with a fused activation 32 CW gate columns.
+    const FixupTile<DT> ft{a.part, out, bias, a.M, a.N, Np, a.ks, a.act, m0, rows,
+                           a.act ? bx * 32 * CW : bx * 64 * CW, a.act ? 8 * CW : 16 * CW};
+    splitk_fixup<64 * NW, DT>(ft, tc, fbase, kslice, a.polls);
+  }
 }
 
 // OCC = workgroups per CU the register budget is cut for (2: 256 registers,
@@ -997,10 +1023,10 @@ hipError_t launch_dt(const GemmPlan& p, const TiledArgs& a, int gpt, hipStream_t
 // activation offsets (bm rows of K elements) stay below 2^31 bytes.
 int64_t tiled_max_k(int bm) { return ((int64_t(1) << 31) - 1) / (2 * (int64_t)bm); }
 
-// (The split K of this kernel reduces in a second kernel, so it needs no
-// arrival counters; `counters` is accepted for the common launch signature.)
+// `counters`: the split tiles' counters (kFixupBytes, awq_fixup.h) for the
+// in-kernel reduction, or null for the reduction kernel.
 hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const void* sr, const void* zr,
-                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* /*counters*/,
+                        const void* bias, void* out, int dtype, const Geom& g, void* ws, int32_t* counters,
                         int act, hipStream_t s) {
   if (p.grid_x * p.grid_y * p.ks >= (int64_t(1) << 24)) return hipErrorInvalidConfiguration;
   TiledArgs a;
@@ -1023,10 +1049,13 @@ hipError_t launch_tiled(const GemmPlan& p, const void* x, const void* w, const v
   a.ktc = p.ktc;
   a.part = (float*)ws;
   a.act = act;
+  const bool fixup = p.ks > 1 && p.fixup && counters != nullptr;
+  a.tcnt = fixup ? (uint32_t*)counters : nullptr;
+  a.polls = p.polls;
   // Groups per 128-row k-tile: 1 for G >= 128 (or one group), else 128 / G.
   const int gpt = (g.NG > 1 && g.G < 128) ? (int)(128 / g.G) : 1;
   hipError_t e = dtype == 0 ? launch_dt<F16>(p, a, gpt, s) : launch_dt<BF16>(p, a, gpt, s);
-  if (e != hipSuccess || p.ks == 1) return e;
+  if (e != hipSuccess || p.ks == 1 || fixup) return e;
   return dtype == 0 ? launch_splitk_reduce<F16>((const float*)ws, bias, out, g, p.ks, act, s)
                     : launch_splitk_reduce<BF16>((const float*)ws, bias, out, g, p.ks, act, s);
 }

@@ -245,12 +245,23 @@ def gemm_kernel(M: int, N: int, K: int, group_size: int, activation: Optional[st
 
 
 class PlanInfo(NamedTuple):
-    kernel: str
+    kernel: str           # kernel kind (KERNEL_NAMES): which family and planner branch
     variant: int
     k_slices: int
     workgroups: int
     threads: int
     workspace_bytes: int
+    function: str = ""    # the __global__ function the GEMM launch runs
+    fixup: bool = False   # split K summed inside the GEMM kernel (no second launch, given counters)
+
+
+def kernel_function(kind: str, variant: int) -> str:
+    """Name of the HIP kernel a plan's GEMM launch runs: the tiled kind runs
+    ``tiled_kernel`` for row-block codes below 1000 (16x16x32 MFMAs) and
+    ``mfma32_kernel`` for the others (32x32x16 MFMAs)."""
+    if kind == "tiled_kernel" and variant >= 1000:
+        return "mfma32_kernel"
+    return kind
 
 
 def plan_info(M: int, N: int, K: int, group_size: int, activation: Optional[str] = None) -> PlanInfo:
@@ -258,15 +269,19 @@ def plan_info(M: int, N: int, K: int, group_size: int, activation: Optional[str]
     G = resolve_group_size(group_size, K)
     info = (ctypes.c_int64 * 6)()
     act = 0 if activation is None else _GATED_ACT[activation]
-    _lib.check(_lib.load().awq_gemm_plan_info(M, N, K, G, act, info), "awq_gemm_plan_info")
-    return PlanInfo(KERNEL_NAMES[int(info[0])], *[int(v) for v in info[1:]])
+    lib = _lib.load()
+    _lib.check(lib.awq_gemm_plan_info(M, N, K, G, act, info), "awq_gemm_plan_info")
+    fixup = _lib.check(lib.awq_gemm_plan_fixup(M, N, K, G, act), "awq_gemm_plan_fixup") == 1
+    kind = KERNEL_NAMES[int(info[0])]
+    return PlanInfo(kind, *[int(v) for v in info[1:]], function=kernel_function(kind, int(info[1])), fixup=fixup)
 
 
 PLAN_KNOBS = {"gemv_max_m": _lib.AWQ_PLAN_GEMV_MAX_M, "gemv_variant": _lib.AWQ_PLAN_GEMV_VARIANT,
               "gemv_ks": _lib.AWQ_PLAN_GEMV_KS, "skinny_variant": _lib.AWQ_PLAN_SKINNY_VARIANT,
               "skinny_ks": _lib.AWQ_PLAN_SKINNY_KS, "tiled_min_m": _lib.AWQ_PLAN_TILED_MIN_M,
               "tiled_bm": _lib.AWQ_PLAN_TILED_BM, "tiled_ks": _lib.AWQ_PLAN_TILED_KS,
-              "kslice_variant": _lib.AWQ_PLAN_KSLICE_VARIANT}
+              "kslice_variant": _lib.AWQ_PLAN_KSLICE_VARIANT, "tiled_fixup": _lib.AWQ_PLAN_TILED_FIXUP,
+              "fixup_polls": _lib.AWQ_PLAN_FIXUP_POLLS}
 
 
 def set_plan_override(knob: str, value: int) -> None:
@@ -294,9 +309,19 @@ def device_cu_count() -> int:
 
 
 def make_counters(N: int, device: torch.device) -> torch.Tensor:
-    """Split-K arrival counters: zeroed once here, left zeroed by every GEMM call."""
+    """Split-K counters (awq_counter_bytes): zeroed once here; every GEMM call leaves them valid for the
+    next, whatever its shape (torch allocations are 512-byte aligned, as the 128 the library needs)."""
     nbytes = _lib.check(_lib.load().awq_counter_bytes(N), "awq_counter_bytes")
     return torch.zeros(nbytes // 4, dtype=torch.int32, device=device)
+
+
+def counters_settled(counters: torch.Tensor) -> bool:
+    """True when no GEMM is in flight on ``counters``: the decode kernels' per-column-tile counters are
+    zero and every split tile of the tiled kernels has as many arrivals as its base (each launch that
+    split a tile advanced both by its k-slice count)."""
+    nt = _lib.AWQ_COUNTER_TILE_BYTES // 4
+    tiles = counters[:nt].view(-1, 32)
+    return bool(torch.equal(tiles[:, 0], tiles[:, 1])) and int(counters[nt:].abs().sum()) == 0
 
 
 # ---------------------------------------------------------------------------
@@ -418,10 +443,12 @@ def _check_counters(counters: torch.Tensor, N: int, device: torch.device) -> Non
         raise ValueError(f"counters must be on {device}, got {counters.device}")
     if not counters.is_contiguous():
         raise ValueError("counters must be contiguous")
-    need = (N + 15) // 16
+    need = _lib.check(_lib.load().awq_counter_bytes(N), "awq_counter_bytes") // 4
     if counters.numel() < need:
         raise ValueError(f"counters must hold at least {need} int32 (awq_counter_bytes({N}) bytes), "
                          f"got {counters.numel()}")
+    if counters.data_ptr() % 128:
+        raise ValueError("counters must be 128-byte aligned")
 
 
 def gemm(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, bias: Optional[torch.Tensor] = None,
@@ -488,11 +515,25 @@ def gemm_noalloc(x: torch.Tensor, r: Repacked, K: int, N: int, group_size: int, 
                                                        or bias.dtype != x.dtype)):
         raise ValueError("x (and bias: N elements of x's dtype) must be contiguous")
     with _on_device(x.device):
+        _noalloc_ready(x.device)
         _lib.check(_lib.load().awq_w4a16_gemm_noalloc(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(),
                                                       _ptr(bias), out.data_ptr(), M, N, K,
                                                       resolve_group_size(group_size, K), dtype_code(x.dtype),
                                                       _stream(x.device)), "awq_w4a16_gemm_noalloc")
     return out
+
+
+_NOALLOC_READY: set = set()
+
+
+def _noalloc_ready(device: torch.device) -> None:
+    """Resolve the device's static scratch ahead of the first call (awq_noalloc_init), unless that
+    call is being captured: then the library's first call puts the counter clearing in the graph."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _NOALLOC_READY or torch.cuda.is_current_stream_capturing():
+        return
+    _lib.check(_lib.load().awq_noalloc_init(_stream(device)), "awq_noalloc_init")
+    _NOALLOC_READY.add(idx)
 
 
 def stream_probe(src: torch.Tensor, nbytes: int, grid: int, block: int, sink: torch.Tensor) -> None:

@@ -55,7 +55,8 @@ def test_size_queries_match_layout(K, N, G):
     assert lib.awq_repacked_weight_bytes(K, N) == sh["w_bytes"]
     assert lib.awq_repacked_scale_bytes(K, N, G) == sh["s_bytes"]
     assert lib.awq_repacked_zero_bytes(K, N, G) == sh["z_bytes"]
-    assert lib.awq_counter_bytes(N) == 4 * ((N + 15) // 16)
+    # the tiled kernels' split-tile counters, then one int32 per column tile
+    assert lib.awq_counter_bytes(N) == _lib.AWQ_COUNTER_TILE_BYTES + 4 * ((N + 15) // 16)
     assert lib.awq_workspace_bytes(0, N, K, G) == 0
 
 
@@ -193,8 +194,48 @@ def test_short_counters_are_reported_before_launch():
     cb = lib.awq_counter_bytes(N)
     st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake, cb - 4, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE and "counters of" in _lib.last_error()
-    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake + 2, cb, None)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake + 64, cb, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE and "aligned" in _lib.last_error()
+
+
+def test_abi_version_and_counter_layout():
+    lib = _lib.load()
+    assert lib.awq_abi_version() == _lib.AWQ_ABI_VERSION == 3
+    assert lib.awq_version().decode().endswith("0.3")
+    # the constants the binding mirrors agree with the library's sizes
+    assert lib.awq_counter_bytes(16) == _lib.AWQ_COUNTER_TILE_BYTES + 4
+    assert lib.awq_counter_bytes(_lib.AWQ_NOALLOC_MAX_N) == _lib.AWQ_COUNTER_TILE_BYTES + _lib.AWQ_NOALLOC_MAX_N // 4
+    # a library of another ABI revision is refused before any symbol is bound
+    import ctypes
+    saved = _lib.AWQ_ABI_VERSION
+    try:
+        _lib.AWQ_ABI_VERSION = 2
+        with pytest.raises(RuntimeError, match="ABI"):
+            _lib._lib, keep = None, _lib._lib
+            try:
+                _lib.load()
+            finally:
+                _lib._lib = keep
+    finally:
+        _lib.AWQ_ABI_VERSION = saved
+    assert isinstance(_lib.load(), ctypes.CDLL)
+
+
+def test_tiled_split_k_accepts_missing_counters():
+    # the tiled kernels take the counters when given (sum in the kernel) and
+    # fall back to a second kernel without them; misaligned ones are refused
+    lib = _lib.load()
+    fake = 0x10000
+    M, N, K = 32, 6144, 2560
+    from sglite_amd import ops
+    info = ops.plan_info(M, N, K, 128)
+    assert info.kernel == "tiled_kernel" and info.k_slices > 1 and info.function == "mfma32_kernel"
+    assert not info.fixup  # opt-in
+    with ops.plan_overrides(tiled_fixup=1):
+        assert ops.plan_info(M, N, K, 128).fixup
+    need = lib.awq_workspace_bytes(M, N, K, 128)
+    st = lib.awq_w4a16_gemm(fake, fake, fake, fake, None, fake, M, N, K, 128, 0, fake, need, fake + 64, 1 << 20, None)
+    assert st == _lib.AWQ_STATUS_WORKSPACE and "128-byte aligned" in _lib.last_error()
 
 
 def test_plan_overrides_and_plan_info():
