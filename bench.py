@@ -94,10 +94,10 @@ def pack_awq_gpu(q: torch.Tensor) -> torch.Tensor:
     return w
 
 
-def make_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device):
+def make_repacked(ops, K: int, N: int, gen: torch.Generator, dev: torch.device, dtype=torch.float16):
     q = torch.randint(0, 16, (K, N), generator=gen, device=dev, dtype=torch.int32)
     z = torch.randint(0, 16, (K // G, N), generator=gen, device=dev, dtype=torch.int32)
-    s = (torch.rand((K // G, N), generator=gen, device=dev) * 0.018 + 0.002).to(torch.float16)
+    s = (torch.rand((K // G, N), generator=gen, device=dev) * 0.018 + 0.002).to(dtype)
     r = ops.repack(pack_awq_gpu(q), pack_awq_gpu(z), s)
     del q, z, s
     return r
@@ -519,9 +519,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> str:
             if r["Counter_Name"] != counter:
                 continue
             name = r["Kernel_Name"]
-            key = next((k for k in ("skinny_kernel", "gemv_kernel", "tiled_kernel", "kslice_kernel") if k in name), None)
-            if key is None and "mfma32_kernel" in name:  # the 32x32-MFMA member of the tiled kind
-                key = "tiled_kernel"
+            key = next((k for k in DECODE_KERNELS if k + "<" in name), None)
             if key is None and "copyBuffer" in name:  # torch's device-to-device copy is a runtime blit
                 key = "copy"
             if key is not None:
@@ -537,7 +535,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> str:
     algo = defaultdict(list)
     for M in M_SET:
         for _, K, N in LAYER:
-            algo[ops.gemm_kernel(M, N, K, G)].append(gemm_bytes(M, N, K))
+            algo[ops.plan_info(M, N, K, G).function].append(gemm_bytes(M, N, K))
     lines = [
         "# HBM traffic of the decode kernels (Qwen3-4B layer, M = 1, 8, 32), rocprofv3 PMC",
         "",
@@ -578,10 +576,9 @@ def committed_traffic(kernel: str):
     return None
 
 
-DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "kslice_kernel")
-# Kernel names of each planner kind in a trace (kind 1 has two kernels).
-KIND_PREFIXES = {"skinny_kernel": ("skinny_kernel<",), "gemv_kernel": ("gemv_kernel<",),
-                 "tiled_kernel": ("tiled_kernel<", "mfma32_kernel<"), "kslice_kernel": ("kslice_kernel<",)}
+# The HIP kernels a decode GEMM launch can run (ops.PlanInfo.function); the
+# tiled kind runs tiled_kernel (16x16x32 MFMAs) or mfma32_kernel (32x32x16).
+DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "kslice_kernel")
 TRACE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "splitk_reduce_kernel", "moe_",
                  "topk_softmax_kernel", "align_kernel", "kslice_kernel")
 
@@ -667,7 +664,7 @@ def bounds_bench(ops, dev: torch.device, reps: int = 7) -> dict:
 
 def _launches_per_call(ops, M: int, N: int, K: int, activation=None) -> int:
     info = ops.plan_info(M, N, K, G, activation)
-    return 2 if info.kernel == "tiled_kernel" and info.k_slices > 1 else 1
+    return 2 if info.kernel == "tiled_kernel" and info.k_slices > 1 and not info.fixup else 1
 
 
 def profile_workload(name: str, ops, dev: torch.device, gen: torch.Generator) -> None:
@@ -799,8 +796,8 @@ def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
             "",
         ]
         for kern in DECODE_KERNELS:
-            pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.gemm_kernel(M, N, K, G) == kern]
-            ds = [d for (k, *_), v in groups.items() if k.startswith(KIND_PREFIXES[kern]) for d in v]
+            pairs = [(M, N, K) for M in M_SET for _, K, N in LAYER if ops.plan_info(M, N, K, G).function == kern]
+            ds = [d for (k, *_), v in groups.items() if k.startswith(kern + "<") for d in v]
             if not pairs or not ds:
                 continue
             mean_b = sum(gemm_bytes(*p) for p in pairs) / len(pairs)
@@ -936,7 +933,7 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
             info = ops.plan_info(M, N, K, G)
             probe = prober.us(b, info.workgroups, info.threads)
             best_us, best_g, best_b = prober.best(b)
-            kern = info.kernel
+            kern = info.function
             lin[name] = {"us": round(us, 3), "GB/s": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                          "kernel": kern, "grid": info.workgroups, "block": info.threads, "k_slices": info.k_slices,
                          "ceiling_us": round(probe, 3), "frac_of_ceiling": round(probe / us, 4),
@@ -971,27 +968,42 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
             "per_m": per_m}
 
 
-# Config 2's batches, plus the decode batches 64..160 that graph capture
-# covers (multiples of 8 up to the largest decode batch).
-LLAMA_M = (1, 16, 64, 128, 160, 256, 2048, 8192)
+# Config 2's batches, the reference's graph-captured decode batches below 16
+# (cuda_graph.py:76: [1, 2, 4] + multiples of 8), and the decode batches
+# 64..160 that graph capture covers.
+LLAMA_M = (1, 2, 4, 8, 16, 64, 128, 160, 256, 2048, 8192)
+
+# One GPU's share of tensor-parallel shards (column-parallel layers split N,
+# row-parallel ones K: weight_loader.py:40-69, linear.py:127-194): the
+# Llama-3.1-70B stack at TP8 and Llama-3-8B at TP2 and TP4.
+TP_SHARDS = {
+    "70b_tp8": [("qkv_proj", 8192, 1280), ("o_proj", 1024, 8192), ("gate_up_proj", 8192, 7168),
+                ("down_proj", 3584, 8192)],
+    "llama3_8b_tp2": [("qkv_proj", 4096, 3072), ("o_proj", 2048, 4096), ("gate_up_proj", 4096, 14336),
+                      ("down_proj", 7168, 4096)],
+    "llama3_8b_tp4": [("qkv_proj", 4096, 1536), ("o_proj", 1024, 4096), ("gate_up_proj", 4096, 7168),
+                      ("down_proj", 3584, 4096)],
+}
+TP_M = (1, 8, 32, 2048)
 
 
-def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
-    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192) and at the
-    decode batches 64, 128 and 160, int4 group 128, fp16.  M <= 256: graphs of back-to-back launches
-    over `copies` weight copies (1.1 GB); M >= 2048: eager calls.  Median over MEDIAN_SAMPLES
-    samples; GB/s against the HBM peak (and the streaming probe's ceiling at M <= 32) and TFLOP/s
-    against the dense fp16 MFMA peak; `bound` is the roofline the layer's arithmetic intensity
-    (flop per algorithmic byte) puts it under."""
-    reps = [{name: make_repacked(ops, K, N, gen, dev) for name, K, N in PREFILL} for _ in range(copies)]
-    cnts = {name: ops.make_counters(N, dev) for name, K, N in PREFILL}
-    xg = torch.Generator(device=dev).manual_seed(3)
+def linears_bench(ops, dev, prober, shapes, Ms, dtype=torch.float16, copies: int = 10, seed: int = 3,
+                  ceilings: bool = True) -> dict:
+    """A set of linears at several M: M <= 256 as graphs of back-to-back launches over `copies`
+    weight copies, larger M as eager calls; median over MEDIAN_SAMPLES samples.  GB/s against the
+    HBM peak (and the streaming probe's ceiling at M <= 32) and TFLOP/s against the dense MFMA peak;
+    `bound` is the roofline the layer's arithmetic intensity (flop per algorithmic byte) puts it
+    under; `kernel` names the HIP kernel the GEMM launch runs."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    reps = [{name: make_repacked(ops, K, N, gen, dev, dtype) for name, K, N in shapes} for _ in range(copies)]
+    cnts = {name: ops.make_counters(N, dev) for name, K, N in shapes}
+    xg = torch.Generator(device=dev).manual_seed(seed + 1)
     res = {}
-    for M in LLAMA_M:
-        xs = {K: torch.randn((M, K), generator=xg, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
-        outs = {name: torch.empty((M, N), dtype=torch.float16, device=dev) for name, _, N in PREFILL}
+    for M in Ms:
+        xs = {K: torch.randn((M, K), generator=xg, device=dev).to(dtype) for K in {k for _, k, _ in shapes}}
+        outs = {name: torch.empty((M, N), dtype=dtype, device=dev) for name, _, N in shapes}
         lin, tb, tf, tt = {}, 0, 0, 0.0
-        for name, K, N in PREFILL:
+        for name, K, N in shapes:
             def call(c, name=name, K=K, N=N):
                 ops.gemm(xs[K], reps[c][name], K, N, G, counters=cnts[name], out=outs[name])
             if M <= 256:
@@ -1007,10 +1019,10 @@ def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
             b, fl = gemm_bytes(M, N, K), 2 * M * N * K
             info = ops.plan_info(M, N, K, G)
             e = {"us": round(us, 2), "GB/s": round(b / us / 1e3, 1), "TFLOP/s": round(fl / us / 1e6, 1),
-                 "kernel": info.kernel, "grid": info.workgroups, "k_slices": info.k_slices}
+                 "kernel": info.function, "grid": info.workgroups, "k_slices": info.k_slices}
             e.update({"frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
                       "frac_mfma": round(fl / us / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4)})
-            if M <= 32:
+            if M <= 32 and ceilings:
                 probe = prober.us(b, info.workgroups, info.threads)
                 e.update({"ceiling_us": round(probe, 3), "frac_of_ceiling": round(probe / us, 4)})
             lin[name] = e
@@ -1023,9 +1035,73 @@ def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
         del xs, outs
     del reps
     torch.cuda.synchronize()
+    return res
+
+
+def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
+    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192), at the
+    graph-captured decode batches 2, 4, 8 and 64, 128, 160; int4 group 128, fp16."""
+    res = linears_bench(ops, dev, prober, PREFILL, LLAMA_M, copies=copies)
     return {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, down 14336x4096), "
                         f"int4 group 128 with zeros, fp16, M in {list(LLAMA_M)}; {copies} weight copies; median of "
                         f"{MEDIAN_SAMPLES}", "per_m": res}
+
+
+def _compact(res: dict) -> dict:
+    """Per-M summary plus each linear's time, rate and kernel (a shorter record)."""
+    out = {}
+    for M, v in res.items():
+        out[M] = {k: v[k] for k in ("us_per_layer", "GB/s", "frac_hbm", "TFLOP/s", "frac_mfma", "bound")}
+        out[M]["linears"] = {n: {k: e[k] for k in ("us", "kernel", "k_slices", "frac_of_ceiling") if k in e}
+                             for n, e in v["linears"].items()}
+    return out
+
+
+def tp_bench(ops, dev, prober) -> dict:
+    """One GPU's share of the tensor-parallel shards (TP_SHARDS) at M = 1, 8, 32 and 2048, fp16."""
+    out = {"workload": "one GPU's shard of column-parallel (N / tp) and row-parallel (K / tp) AWQ linears, "
+                       "int4 group 128 with zeros, fp16; Llama-3.1-70B at TP8 (qkv 8192x1280, o 1024x8192, "
+                       "gate_up 8192x7168, down 3584x8192), Llama-3-8B at TP2 and TP4; the all-reduce of the "
+                       "row-parallel partials is not timed (one GPU)"}
+    for name, shapes in TP_SHARDS.items():
+        out[name] = _compact(linears_bench(ops, dev, prober, shapes, TP_M, copies=10, seed=11))
+    return out
+
+
+def bf16_bench(ops, dev, prober) -> dict:
+    """bf16 activations and scales (the reference engine's default dtype, llm/llm.py:34, with
+    scales cast to it, engine.py:171): the Qwen3-4B decode layer at M = 1, 8, 32 and the
+    Llama-3-8B linears at M = 2048."""
+    dec = linears_bench(ops, dev, prober, LAYER, M_SET, dtype=torch.bfloat16, copies=12, seed=21)
+    pf = linears_bench(ops, dev, prober, PREFILL, (PREFILL_M,), dtype=torch.bfloat16, copies=3, seed=23)
+    return {"workload": "bf16 activations and scales: Qwen3-4B decode layer (M = 1, 8, 32) and Llama-3-8B linears "
+                        f"at M = {PREFILL_M}, int4 group 128 with zeros",
+            "decode": _compact(dec), "prefill": _compact(pf)}
+
+
+def hipblaslt_bench(ops, dev, reps: int = 15) -> dict:
+    """The vendor library's dense fp16 GEMM (torch.matmul, hipBLASLt on ROCm) on the Llama-3-8B
+    linears at M = 2048 and 8192 with fp16 weights of the same shapes: the dense-GEMM rate the
+    W4A16 kernels (which also dequantise every weight) are compared with."""
+    gen = torch.Generator(device=dev).manual_seed(31)
+    out = {"library": "torch.matmul (hipBLASLt), fp16 dense weights [K, N], fp32 accumulation"}
+    for M in (PREFILL_M, 8192):
+        tt, tf, lin = 0.0, 0, {}
+        for name, K, N in PREFILL:
+            x = torch.randn((M, K), generator=gen, device=dev).to(torch.float16)
+            w = (torch.randn((K, N), generator=gen, device=dev) * 0.02).to(torch.float16)
+            y = torch.empty((M, N), dtype=torch.float16, device=dev)
+            for _ in range(3):
+                torch.matmul(x, w, out=y)
+            us = median(call_samples(lambda: torch.matmul(x, w, out=y), reps)) * 1e3
+            fl = 2 * M * N * K
+            lin[name] = {"us": round(us, 2), "TFLOP/s": round(fl / us / 1e6, 1)}
+            tt, tf = tt + us, tf + fl
+            del x, w, y
+        out[str(M)] = {"TFLOP/s": round(tf / tt / 1e6, 1), "frac": round(tf / tt / 1e6 / MFMA_FP16_PEAK_TFLOPS, 4),
+                       "linears": lin}
+    torch.cuda.synchronize()
+    return out
 
 
 def main() -> int:
@@ -1039,6 +1115,8 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-mlp", action="store_true", help="skip the fused/unfused gated MLP block comparison")
     ap.add_argument("--no-stack", action="store_true", help="skip the 70B-shaped stack (35.6 GB of weights)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the tensor-parallel shard, bf16 and hipBLASLt comparison sections")
     ap.add_argument("--no-decode", action="store_true",
                     help="skip the decode step (profiling runs of the other sections; no value is reported)")
     ap.add_argument("--rocprof-summary", nargs=2, metavar=("SECTION", "TRACE_DIR"),
@@ -1116,10 +1194,15 @@ def main() -> int:
     del reps
     torch.cuda.synchronize()
 
-    llama = None
+    llama = tp = bf16 = None
     if not args.no_prefill:
         progress("llama3-8b sweep")
         llama = llama_bench(ops, dev, gen, prober)
+    if not args.no_extra:
+        progress("tensor-parallel shards")
+        tp = tp_bench(ops, dev, prober)
+        progress("bf16")
+        bf16 = bf16_bench(ops, dev, prober)
     del prober
     torch.cuda.synchronize()
     prefill = None
@@ -1127,8 +1210,9 @@ def main() -> int:
         pm = llama["per_m"][str(PREFILL_M)]
         prefill = {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, "
                                f"down 14336x4096) at M={PREFILL_M}, fp16", "TFLOP/s": pm["TFLOP/s"],
-                   "peak": MFMA_FP16_PEAK_TFLOPS, "frac": pm["frac_mfma"], "kernel": "tiled_kernel",
-                   "linears": {k: {"us": v["us"], "TFLOP/s": v["TFLOP/s"]} for k, v in pm["linears"].items()},
+                   "peak": MFMA_FP16_PEAK_TFLOPS, "frac": pm["frac_mfma"],
+                   "linears": {k: {"us": v["us"], "TFLOP/s": v["TFLOP/s"], "kernel": v["kernel"]}
+                               for k, v in pm["linears"].items()},
                    "m8192": {"TFLOP/s": llama["per_m"]["8192"]["TFLOP/s"],
                              "frac": llama["per_m"]["8192"]["frac_mfma"]}}
 
@@ -1147,6 +1231,9 @@ def main() -> int:
     if not args.no_prefill:
         progress("mfma probe")
         bounds = bounds_bench(ops, dev)
+        if not args.no_extra:
+            progress("hipblaslt")
+            bounds["hipblaslt_dense_fp16"] = hipblaslt_bench(ops, dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -1176,14 +1263,18 @@ def main() -> int:
                    "ms_per_step_mean": None if dec is None else round(dec["ms_per_step_mean"], 5)},
         "roofline": None if dec is None else dec["roofline"],
         "cpu_baseline": cpu,
-        "decode_kernels": None if dec is None else dec["kernels"],
-        "per_m": None if dec is None else dec["per_m"],
-        "prefill": prefill,
+        # The long sections first, the decode summary last: the end of the
+        # line is what a truncated log keeps.
         "llama3_8b": llama,
-        "mlp": mlp,
-        "moe": moe,
+        "tp_shards": tp,
+        "bf16": bf16,
         "stack70b": stack,
         "bounds": bounds,
+        "moe": moe,
+        "mlp": mlp,
+        "prefill": prefill,
+        "decode_kernels": None if dec is None else dec["kernels"],
+        "per_m": None if dec is None else dec["per_m"],
     }
     print(json.dumps(line))
     return 0

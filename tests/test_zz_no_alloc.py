@@ -92,3 +92,76 @@ def test_noalloc_python_wrapper_and_limits():
     big = torch.empty((4096, K), dtype=torch.float16, device=DEV)
     with pytest.raises(RuntimeError, match="scratch"):
         ops.gemm_noalloc(big, r, K, N, 128, torch.empty((4096, N), dtype=torch.float16, device=DEV))
+
+
+_FIRST_CALL = r"""
+import sys, torch
+sys.path.insert(0, {root!r})
+from oracle import awq_oracle as oracle
+from sglite_amd import _lib, ops
+captured = {captured!r}
+dev = torch.device("cuda:0")
+K, N, G = 28672, 512, 128          # split K on the decode kernels: counters in the scratch
+lib = _lib.load()
+t = oracle.make_awq_linear(K, N, G, seed=5)
+r = ops.repack(t["qweight"].to(dev), t["qzeros"].to(dev), t["scales"].to(dev))  # loads the code object
+xs = [oracle.make_activation(M, K, seed=M).to(dev) for M in (32, 8)]
+outs = [torch.full((x.shape[0], N), float("nan"), dtype=torch.float16, device=dev) for x in xs]
+torch.cuda.synchronize()
+
+
+def calls(stream):
+    for x, out in zip(xs, outs):   # the first noalloc calls of the process
+        st = lib.awq_w4a16_gemm_noalloc(x.data_ptr(), r.w.data_ptr(), r.s.data_ptr(), r.z.data_ptr(), None,
+                                        out.data_ptr(), x.shape[0], N, K, G, 0, stream)
+        assert st == 0, _lib.last_error()
+
+
+if captured:
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        calls(s.cuda_stream)
+    torch.cuda.synchronize()
+else:
+    # The HIP runtime maps the library's static scratch (and loads kernel
+    # code) on first use; awq_noalloc_init and one ordinary call of each
+    # shape take that cost before the measured calls.
+    want = [ops.gemm(x, r, K, N, G, counters=ops.make_counters(N, dev)) for x in xs]
+    assert lib.awq_noalloc_init(torch.cuda.current_stream().cuda_stream) == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    calls(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free0 == free1, ("the call allocated device memory", free0, free1)
+want = [ops.gemm(x, r, K, N, G, counters=ops.make_counters(N, dev)) for x in xs]
+for rep in range(3 if captured else 1):
+    if captured:
+        for out in outs:
+            out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+    for out, w in zip(outs, want):
+        assert torch.equal(out, w), rep
+print("first-call ok")
+"""
+
+
+@pytest.mark.parametrize("captured", [True, False])
+def test_noalloc_first_call_in_a_fresh_process(captured):
+    """The first noalloc call of a process under graph capture (the counter
+    clearing then becomes a node of the graph): every replay equals the
+    existing entry point's output bit for bit.  Eager, after awq_noalloc_init:
+    the calls leave the device's free memory unchanged and equal the existing
+    entry point's output."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = _FIRST_CALL.format(root=root, captured=captured)
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert "first-call ok" in res.stdout
