@@ -236,7 +236,7 @@ def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, re
     H, I = 2560, 9728
     gu = [make_repacked(ops, H, 2 * I, gen, dev) for _ in range(copies)]
     dn = [make_repacked(ops, I, H, gen, dev) for _ in range(copies)]
-    cg, cd = ops.make_counters(2 * I, dev), ops.make_counters(H, dev)
+    cg, cd, cm = ops.make_counters(2 * I, dev), ops.make_counters(H, dev), ops.make_mlp_counters(dev)
     res = {}
     for M in M_SET:
         x = torch.randn((M, H), generator=gen, device=dev).to(torch.float16)
@@ -253,16 +253,27 @@ def mlp_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 12, re
             ops.gemm(x, gu[c], H, 2 * I, G, counters=cg, out=h, activation="silu")
             ops.gemm(h, dn[c], I, H, G, counters=cd, out=o)
 
+        def one_launch(c):
+            ops.gated_mlp(x, gu[c], dn[c], H, I, G, cm, "silu", out=o)
+
+        plan = ops.gated_mlp_plan(M, H, I, G)
+        forms = [("unfused", unfused), ("fused", fused)] + ([("one_launch", one_launch)] if plan else [])
         t = {}
-        for name, fn in (("unfused", unfused), ("fused", fused)):
+        for name, fn in forms:
             g = graph_of(lambda: [fn(c) for c in range(copies)])
             time_replays([g], 3)
             t[name] = median(replay_samples([g], reps)) * 1e3 / copies
-        res[str(M)] = {"fused_us": round(t["fused"], 2), "unfused_us": round(t["unfused"], 2),
-                       "speedup": round(t["unfused"] / t["fused"], 3)}
+        r = {"fused_us": round(t["fused"], 2), "unfused_us": round(t["unfused"], 2),
+             "speedup": round(t["unfused"] / t["fused"], 3)}
+        if plan:
+            ops.mlp_check(cm)  # no workgroup gave up waiting in any of the timed calls
+            r.update({"one_launch_us": round(t["one_launch"], 2), "one_launch_workgroups": plan.workgroups,
+                      "one_launch_vs_fused": round(t["fused"] / t["one_launch"], 3)})
+        res[str(M)] = r
     return {"workload": "Qwen3-4B gated MLP block: gate_up 2560x19456 + silu(gate)*up + down 9728x2560, int4 group "
                         "128, fp16; fused = activation in the gate_up GEMM epilogue, unfused = torch silu and mul "
-                        "between the GEMMs", "per_m": res}
+                        "between the GEMMs, one_launch = the whole block as one kernel (awq_gated_mlp, M <= 16)",
+            "per_m": res}
 
 
 def moe_bench(ops, dev: torch.device, gen: torch.Generator, copies: int = 3, reps: int = MEDIAN_SAMPLES) -> dict:

@@ -58,9 +58,11 @@ const char* awq_version(void);
  *   3  awq_counter_bytes(N) covers the tiled kernels' split-tile counters
  *      too (AWQ_COUNTER_TILE_BYTES ahead of the per-column-tile counters),
  *      counters must be 128-byte aligned; awq_noalloc_init and the planner
- *      knobs AWQ_PLAN_TILED_FIXUP / AWQ_PLAN_FIXUP_POLLS are new.
+ *      knobs AWQ_PLAN_TILED_FIXUP / AWQ_PLAN_FIXUP_POLLS are new;
+ *   4  the gated MLP block (awq_gated_mlp and its plan, workspace and error
+ *      calls) is new.
  * No counterpart in the reference (its kernels are Python and Triton). */
-#define AWQ_ABI_VERSION 3
+#define AWQ_ABI_VERSION 4
 int awq_abi_version(void);
 
 /* ---- post-load repack ------------------------------------------------------
@@ -185,6 +187,54 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
                        int64_t M, int64_t N, int64_t K, int64_t G, int dtype, int activation, void* ws,
                        int64_t ws_bytes, int32_t* counters, int64_t counter_bytes, awq_stream_t stream);
 
+/* ---- gated MLP block in one launch -------------------------------------------
+ * out[M, H] = down(act(x @ W_gate) * (x @ W_up)) for decode batches: the
+ * GatedMLP forward (python/sglite/srt/model_executor/models/blocks.py:51-57:
+ * gate_up_proj, silu_and_mul / gelu_and_mul, down_proj) as one kernel whose
+ * down-projection weight loads are issued before the gate/up outputs exist.
+ *   x        [M, H], 16-byte aligned; out [M, H], 8-byte aligned
+ *   gu_*     the merged gate/up projection repacked as K = H, N = 2I (gate
+ *            columns first, then up: MergedColumnParallelLinear's layout)
+ *   dn_*     the down projection repacked as K = I, N = H
+ *   G == 128, no bias; each gate / up value is rounded to the dtype and
+ *   act(gate) * up rounded once, as awq_w4a16_gemm_act stores it, and the
+ *   down projection's fp32 k-slice sums are added in a fixed order.
+ *   ws       awq_gated_mlp_workspace_bytes bytes, 256-byte aligned
+ *   counters AWQ_MLP_COUNTER_BYTES bytes, 128-byte aligned, zero before the
+ *            first call and then left alone (every call leaves them valid
+ *            for the next; calls that share them must be stream-ordered)
+ *   polls    how often a workgroup polls the arrival count of its k-slice of
+ *            the intermediate (the workgroups that write that slice) before
+ *            it gives up (negative: AWQ_MLP_DEFAULT_POLLS; 0: only each
+ *            slice's last arrival proceeds).  A workgroup that gives up counts
+ *            itself in word 2 of the counters and skips the down projection;
+ *            every workgroup still exits and the counters stay valid, but
+ *            that call's output is wrong: awq_gated_mlp_take_errors reports it.
+ * The grid is one workgroup per CU at most, never more than the device's
+ * occupancy query for the kernel allows at once, so on an otherwise idle
+ * device no wait lasts longer than the slowest workgroup's gate/up work.
+ * Shapes outside the built forms (M > 16, H > 4096, I / 16 tiles beyond four
+ * per workgroup, ...) return AWQ_STATUS_UNSUPPORTED: awq_gated_mlp_plan
+ * tells beforehand, and the caller runs awq_w4a16_gemm_act and
+ * awq_w4a16_gemm instead.  No counterpart in the reference: a fusion of its
+ * GatedMLP calls. */
+#define AWQ_MLP_COUNTER_BYTES (64ll << 10)
+#define AWQ_MLP_DEFAULT_POLLS (1 << 15)
+/* 1 if awq_gated_mlp runs this shape on the current device, 0 if not;
+ * info (8 entries, may be null): workgroups, down k-slices, down column tiles
+ * per group, column groups, gate tiles per workgroup, down k-tiles per slice,
+ * LDS bytes, workspace bytes. */
+int awq_gated_mlp_plan(int64_t M, int64_t H, int64_t I, int64_t G, int dtype, int64_t* info);
+int64_t awq_gated_mlp_workspace_bytes(int64_t M, int64_t H, int64_t I, int64_t G, int dtype);
+int awq_gated_mlp(const void* x, const void* gu_w, const void* gu_s, const void* gu_z, const void* dn_w,
+                  const void* dn_s, const void* dn_z, void* out, int64_t M, int64_t H, int64_t I, int64_t G, int dtype,
+                  int activation, int polls, void* ws, int64_t ws_bytes, int32_t* counters, int64_t counter_bytes,
+                  awq_stream_t stream);
+/* Synchronizes `stream`, returns the number of workgroups that gave up
+ * waiting since the last call (>= 0) and clears the count.  Not while the
+ * stream is being captured. */
+int64_t awq_gated_mlp_take_errors(int32_t* counters, int64_t counter_bytes, awq_stream_t stream);
+
 /* ---- planner overrides (tests and sweeps) -----------------------------------
  * Force a kernel choice or split for every later GEMM of the process (all
  * threads), e.g. to run each kernel instantiation against the oracle.  The
@@ -207,9 +257,9 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
  *   AWQ_PLAN_TILED_KS        tiled k-slices
  *   AWQ_PLAN_KSLICE_VARIANT  k-slice decode-kernel shape wn*100 + wk*10 + kpw
  *                            (M <= 32; any other value leaves the plan alone)
- *   AWQ_PLAN_TILED_FIXUP     0: split-K tiled plans sum their k-slices in a
- *                            second kernel (default: inside the GEMM kernel,
- *                            when the counters are given)
+ *   AWQ_PLAN_TILED_FIXUP     1: split-K tiled plans sum their k-slices inside
+ *                            the GEMM kernel when the counters are given
+ *                            (default 0: in a second kernel)
  *   AWQ_PLAN_FIXUP_POLLS     how often a k-slice workgroup polls for its
  *                            tile's other slices before it leaves the sum to
  *                            the last one (0: never waits) */

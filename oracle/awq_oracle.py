@@ -21,6 +21,10 @@ Reference functions restated here (paths relative to
                        activation dtype.  The contract accumulates in fp32 (the
                        Marlin path's ``use_fp32_reduce=True``,
                        marlin_utils.py:16, 408), not the Triton fallback's fp16.
+* gated MLP block   -- models/blocks.py:51-57: gate_up_proj (the merged
+                       projection, gate columns first), silu_and_mul /
+                       gelu_and_mul (layers/activation.py:11-23) on the rounded
+                       GEMM output, rounded once, then down_proj.
 * fused MoE         -- layers/fused_moe/fused.py:11-31 (softmax top-k and
                        renormalisation), fused.py:101-202 (GEMM1, silu_and_mul
                        with the gate half first, GEMM2 times the routed weight
@@ -40,6 +44,10 @@ How each part is pinned (tests/test_oracle.py):
                       products with s=1, z=0; one-hot rows give rows of W.
   repack/unrepack     round trip on random and ragged shapes; the repacked
                       dequantisation equals ``dequantize``.
+  gated_mlp_awq       in fp32 activations (no rounding between the steps)
+                      against the dense GatedMLP layer of the package run on
+                      the dequantized weights, and at fp16 against the steps
+                      composed by hand with a swapped gate/up order failing.
   MoE                 explicit per-(token, slot) loops against the vectorised
                       form; softmax/top-k are torch's textbook routines.
 The reference's own tests are not shipped (its .gitignore lists ``tests``), so
@@ -305,6 +313,25 @@ def gelu_and_mul(h: torch.Tensor) -> torch.Tensor:
 
 
 _ACT = {"silu": silu_and_mul, "gelu": gelu_and_mul}
+
+
+def gated_mlp_dequantized(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
+                          activation: str = "silu") -> torch.Tensor:
+    """GatedMLP.forward (blocks.py:51-57) on dequantized weights ([H, 2I] gate columns first, [I, H]):
+    y = rnd(x @ W_gate_up) in fp32, h = rnd(act(gate) * up), out = rnd(h @ W_down)."""
+    dt = x.dtype
+    y = (x.detach().cpu().float() @ w_gate_up.float()).to(dt)
+    h = _ACT[activation](y).to(dt)
+    return (h.float() @ w_down.float()).to(dt)
+
+
+def gated_mlp_awq(x: torch.Tensor, gate_up: Dict[str, torch.Tensor], down: Dict[str, torch.Tensor],
+                  group_size: int, activation: str = "silu") -> torch.Tensor:
+    """GatedMLP.forward on AWQ weights: :func:`gated_mlp_dequantized` of the :func:`dequantize`
+    weights, so each GEMM is exactly :func:`awq_gemm` (no bias)."""
+    wgu = dequantize(gate_up["qweight"], gate_up["qzeros"], gate_up["scales"], group_size)
+    wdn = dequantize(down["qweight"], down["qzeros"], down["scales"], group_size)
+    return gated_mlp_dequantized(x, wgu, wdn, activation)
 
 
 def moe_align_block_size(topk_ids, block_size: int, num_experts: int):

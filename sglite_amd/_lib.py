@@ -50,6 +50,11 @@ SIGNATURES = {
     "awq_gemm_kernel_kind_act": (_int, [_i64, _i64, _i64, _i64]),
     "awq_w4a16_gemm_act": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _i64, _vp,
                                   _i64, _vp]),
+    "awq_gated_mlp_plan": (_int, [_i64, _i64, _i64, _i64, _int, ctypes.POINTER(_i64)]),
+    "awq_gated_mlp_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "awq_gated_mlp": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _int, _vp,
+                             _i64, _vp, _i64, _vp]),
+    "awq_gated_mlp_take_errors": (_i64, [_vp, _i64, _vp]),
     "awq_set_plan_override": (_int, [_int, _int]),
     "awq_clear_plan_overrides": (None, []),
     "awq_device_cu_count": (_int, []),
@@ -84,9 +89,13 @@ AWQ_PLAN_TILED_FIXUP = 9
 AWQ_PLAN_FIXUP_POLLS = 10
 
 # The header revision this binding follows (AWQ_ABI_VERSION).
-AWQ_ABI_VERSION = 3
+AWQ_ABI_VERSION = 4
 # Split-tile counters ahead of the per-column-tile counters (AWQ_COUNTER_TILE_BYTES).
 AWQ_COUNTER_TILE_BYTES = 64 << 10
+
+# Counters of the one-launch gated MLP block (AWQ_MLP_COUNTER_BYTES) and its default poll bound.
+AWQ_MLP_COUNTER_BYTES = 64 << 10
+AWQ_MLP_DEFAULT_POLLS = 1 << 15
 
 AWQ_NOALLOC_WORKSPACE_BYTES = 64 << 20
 AWQ_NOALLOC_MAX_N = 1 << 20

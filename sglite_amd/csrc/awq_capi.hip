@@ -80,6 +80,8 @@ int check_shape(int64_t K, int64_t N, int64_t G, int dtype, int64_t* G_out) {
 // given (else a second kernel sums the k-slices); the others need them.
 constexpr int64_t counter_bytes_for(int64_t N) { return kFixupBytes + ((N + 15) / 16) * 4; }
 static_assert(AWQ_COUNTER_TILE_BYTES == kFixupBytes, "header and kernels agree on the tile counters");
+static_assert(AWQ_MLP_COUNTER_BYTES == kMlpCounterBytes && AWQ_MLP_DEFAULT_POLLS == kMlpDefaultPolls,
+              "header and kernel agree on the gated MLP counters");
 
 int check_counters(const GemmPlan& p, int64_t N, const int32_t* counters, int64_t counter_bytes, const char* who) {
   if (p.kind == 1) {
@@ -188,7 +190,7 @@ extern "C" {
 
 const char* awq_last_error(void) { return g_last_error.c_str(); }
 
-const char* awq_version(void) { return "sglite-awq-gfx950 0.3"; }
+const char* awq_version(void) { return "sglite-awq-gfx950 0.4"; }
 
 int awq_abi_version(void) { return AWQ_ABI_VERSION; }
 
@@ -409,6 +411,101 @@ int awq_w4a16_gemm_act(const void* x, const void* w, const void* s, const void* 
   return hip_status(launch_gemm(p, x, w, s, z, bias, out, dtype, g, ws, counters, counters ? counter_bytes : 0, act,
                                 (hipStream_t)stream),
                     "awq_w4a16_gemm_act launch");
+}
+
+int awq_gated_mlp_plan(int64_t M, int64_t H, int64_t I, int64_t G, int dtype, int64_t* info) {
+  int64_t Gr = 0;
+  int st = check_shape(H, 2 * I, G, dtype, &Gr);
+  if (st == 0) st = check_shape(I, H, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (M <= 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be positive, got %lld", (long long)M);
+  const MlpPlan p = plan_mlp(M, H, I, G, dtype);
+  if (info) {
+    const int64_t v[8] = {p.P, p.S, p.C, p.groups, p.npw, p.nk, p.lds, p.ws_bytes};
+    for (int i = 0; i < 8; ++i) info[i] = p.ok ? v[i] : 0;
+  }
+  ok();
+  return p.ok;
+}
+
+int64_t awq_gated_mlp_workspace_bytes(int64_t M, int64_t H, int64_t I, int64_t G, int dtype) {
+  int64_t Gr = 0;
+  int st = check_shape(H, 2 * I, G, dtype, &Gr);
+  if (st == 0) st = check_shape(I, H, G, dtype, &Gr);
+  if (st != 0) return st;
+  const MlpPlan p = plan_mlp(M, H, I, G, dtype, /*query_device=*/false);
+  if (!p.ok)
+    return fail(AWQ_STATUS_UNSUPPORTED, "awq_gated_mlp: M=%lld H=%lld I=%lld G=%lld is outside the built forms",
+                (long long)M, (long long)H, (long long)I, (long long)G);
+  ok();
+  return p.ws_bytes;
+}
+
+int awq_gated_mlp(const void* x, const void* gu_w, const void* gu_s, const void* gu_z, const void* dn_w,
+                  const void* dn_s, const void* dn_z, void* out, int64_t M, int64_t H, int64_t I, int64_t G, int dtype,
+                  int activation, int polls, void* ws, int64_t ws_bytes, int32_t* counters, int64_t counter_bytes,
+                  awq_stream_t stream) {
+  const TraceRange range("awq_gated_mlp");
+  const char* who = "awq_gated_mlp";
+  int64_t Gr = 0;
+  int st = check_shape(H, 2 * I, G, dtype, &Gr);
+  if (st == 0) st = check_shape(I, H, G, dtype, &Gr);
+  if (st != 0) return st;
+  if (activation != AWQ_ACT_SILU && activation != AWQ_ACT_GELU)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: activation must be AWQ_ACT_SILU or AWQ_ACT_GELU, got %d", who,
+                activation);
+  if (M < 0) return fail(AWQ_STATUS_INVALID_ARGUMENT, "M must be non-negative, got %lld", (long long)M);
+  if (M == 0) return ok();
+  if (!x || !gu_w || !gu_s || !gu_z || !dn_w || !dn_s || !dn_z || !out)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: null pointer argument", who);
+  if (!aligned(x, 16)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: x must be 16-byte aligned", who);
+  if (!aligned(out, 8)) return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: out must be 8-byte aligned", who);
+  if (!aligned(gu_w, 16) || !aligned(gu_s, 16) || !aligned(gu_z, 16) || !aligned(dn_w, 16) || !aligned(dn_s, 16) ||
+      !aligned(dn_z, 16))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: repacked buffers must be 16-byte aligned", who);
+  const MlpPlan shape = plan_mlp(M, H, I, G, dtype, /*query_device=*/false);
+  if (!shape.ok)
+    return fail(AWQ_STATUS_UNSUPPORTED, "%s: M=%lld H=%lld I=%lld G=%lld is outside the built forms", who,
+                (long long)M, (long long)H, (long long)I, (long long)G);
+  if (!ws || ws_bytes < shape.ws_bytes)
+    return fail(AWQ_STATUS_WORKSPACE, "%s: workspace of %lld bytes needed, %lld given", who,
+                (long long)shape.ws_bytes, (long long)(ws ? ws_bytes : 0));
+  if (!aligned(ws, 256)) return fail(AWQ_STATUS_WORKSPACE, "%s: workspace must be 256-byte aligned", who);
+  if (!counters || counter_bytes < AWQ_MLP_COUNTER_BYTES)
+    return fail(AWQ_STATUS_WORKSPACE, "%s: counters of %lld bytes needed, %lld given", who,
+                (long long)AWQ_MLP_COUNTER_BYTES, (long long)(counters ? counter_bytes : 0));
+  if (!aligned(counters, 128)) return fail(AWQ_STATUS_WORKSPACE, "%s: counters must be 128-byte aligned", who);
+  const MlpPlan p = plan_mlp(M, H, I, G, dtype);
+  if (!p.ok)
+    return fail(AWQ_STATUS_UNSUPPORTED, "%s: the device does not keep the %lld-workgroup grid resident", who,
+                (long long)shape.P);
+  const int act = activation == AWQ_ACT_SILU ? kActSilu : kActGelu;
+  return hip_status(launch_mlp(p, x, gu_w, gu_s, gu_z, dn_w, dn_s, dn_z, out, M, H, I, dtype, act, ws, counters,
+                               polls < 0 ? kMlpDefaultPolls : polls, (hipStream_t)stream),
+                    "awq_gated_mlp launch");
+}
+
+int64_t awq_gated_mlp_take_errors(int32_t* counters, int64_t counter_bytes, awq_stream_t stream) {
+  const char* who = "awq_gated_mlp_take_errors";
+  if (!counters || counter_bytes < AWQ_MLP_COUNTER_BYTES || !aligned(counters, 128))
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: counters of %lld bytes, 128-byte aligned, needed", who,
+                (long long)AWQ_MLP_COUNTER_BYTES);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess)
+    return fail(AWQ_STATUS_HIP_ERROR, "%s: hipStreamIsCapturing failed", who);
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(AWQ_STATUS_INVALID_ARGUMENT, "%s: the stream is being captured", who);
+  int32_t n = 0;
+  hipError_t e = hipMemcpyAsync(&n, counters + 2, 4, hipMemcpyDeviceToHost, (hipStream_t)stream);
+  if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  if (e == hipSuccess && n != 0) {
+    const int32_t zero = 0;
+    e = hipMemcpyAsync(counters + 2, &zero, 4, hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
+  }
+  if (e != hipSuccess) return fail(AWQ_STATUS_HIP_ERROR, "%s: %s", who, hipGetErrorString(e));
+  ok();
+  return (int64_t)(uint32_t)n;
 }
 
 int awq_set_plan_override(int knob, int value) {

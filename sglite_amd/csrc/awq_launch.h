@@ -123,4 +123,28 @@ int plan_threads(const GemmPlan& p);
 
 hipError_t launch_moe_sum(const void* in, void* out, int64_t T, int64_t k, int64_t H, int dtype, hipStream_t s);
 
+// Gated MLP block in one launch (awq_mlp.hip).  Counters: 128-byte slots of
+// 32 words; word 2 of slot 0 counts workgroups that gave up waiting, slot
+// 1 + s is k-slice s's barrier, slot 1 + S + g column group g's.
+constexpr int64_t kMlpCounterBytes = 64 << 10;
+constexpr int kMlpDefaultPolls = 1 << 15;
+struct MlpPlan {
+  int ok;         // 0: outside the built forms (the caller runs the two GEMMs)
+  int form;       // kernel instantiation
+  int64_t P;      // workgroups (one per CU at most)
+  int64_t S;      // k-slices of the down projection
+  int64_t C;      // down column tiles per column group
+  int64_t groups; // column groups (P = groups * S)
+  int64_t npw;    // gate tiles per workgroup (of its k-slice)
+  int64_t nk;     // down k-tiles per slice
+  int64_t lds;    // dynamic LDS bytes
+  int64_t h_bytes, ws_bytes;  // intermediate, then fp32 partials
+};
+// query_device: also check the grid against the device's occupancy for the
+// kernel (false: the shape rules alone, for a host without a GPU).
+MlpPlan plan_mlp(int64_t M, int64_t H, int64_t I, int64_t G, int dtype, bool query_device = true);
+hipError_t launch_mlp(const MlpPlan& p, const void* x, const void* gw, const void* gs, const void* gz, const void* dw,
+                      const void* ds, const void* dz, void* out, int64_t M, int64_t H, int64_t I, int dtype, int act,
+                      void* ws, int32_t* counters, int polls, hipStream_t s);
+
 }  // namespace sgl_awq

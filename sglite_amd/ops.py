@@ -536,6 +536,131 @@ def _noalloc_ready(device: torch.device) -> None:
     _NOALLOC_READY.add(idx)
 
 
+# ---------------------------------------------------------------------------
+# Gated MLP block in one launch (awq_gated_mlp): gate_up -> act(gate) * up ->
+# down for decode batches, GatedMLP.forward (blocks.py:51-57) as one kernel.
+# ---------------------------------------------------------------------------
+
+
+class MlpPlan(NamedTuple):
+    workgroups: int
+    k_slices: int         # k-slices of the down projection
+    tiles_per_group: int  # down column tiles per column group
+    groups: int           # down column groups
+    gate_tiles: int       # gate tiles per workgroup
+    k_tiles: int          # down k-tiles per slice
+    lds_bytes: int
+    ws_bytes: int
+
+
+def gated_mlp_plan(M: int, H: int, I: int, group_size: int, dtype: torch.dtype = torch.float16) -> Optional[MlpPlan]:
+    """The one-launch plan for this block on the current device, or None when the shape is outside
+    the built forms (then the block runs as its two GEMMs)."""
+    info = (ctypes.c_int64 * 8)()
+    r = _lib.check(_lib.load().awq_gated_mlp_plan(M, H, I, resolve_group_size(group_size, H), dtype_code(dtype),
+                                                  info), "awq_gated_mlp_plan")
+    return MlpPlan(*[int(v) for v in info]) if r == 1 else None
+
+
+def make_mlp_counters(device: torch.device) -> torch.Tensor:
+    """Counters of the one-launch gated MLP (AWQ_MLP_COUNTER_BYTES, zeroed once here; every call
+    leaves them valid for the next).  Calls that share them must be ordered on one stream."""
+    return torch.zeros(_lib.AWQ_MLP_COUNTER_BYTES // 4, dtype=torch.int32, device=device)
+
+
+def mlp_counters_settled(counters: torch.Tensor) -> bool:
+    """True when no one-launch gated MLP is in flight on ``counters``: every 128-byte slot has as many
+    arrivals as its base (each launch advanced both by its arrivals)."""
+    slots = counters.view(-1, 32)
+    return bool(torch.equal(slots[:, 0], slots[:, 1]))
+
+
+def mlp_take_errors(counters: torch.Tensor) -> int:
+    """Synchronize the current stream and return (and clear) the number of workgroups that gave up
+    waiting for their k-slice of the intermediate since the last check."""
+    _require_cuda(counters)
+    with _on_device(counters.device):
+        return _lib.check(_lib.load().awq_gated_mlp_take_errors(counters.data_ptr(), counters.numel() * 4,
+                                                                _stream(counters.device)), "awq_gated_mlp_take_errors")
+
+
+def mlp_check(counters: torch.Tensor) -> None:
+    """Raise AWQKernelError when a one-launch gated MLP on ``counters`` gave up waiting (its output
+    was wrong) since the last check; the counters stay valid for further calls."""
+    n = mlp_take_errors(counters)
+    if n:
+        raise _lib.AWQKernelError(f"awq_gated_mlp: {n} workgroup(s) gave up waiting for the intermediate; "
+                                  "the outputs of those calls are invalid")
+
+
+def _mlp_launch(x: torch.Tensor, gw: torch.Tensor, gs: torch.Tensor, gz: torch.Tensor, dw: torch.Tensor,
+                ds: torch.Tensor, dz: torch.Tensor, counters: torch.Tensor, out: torch.Tensor, H: int, I: int,
+                G: int, activation: str, polls: int) -> None:
+    M = x.shape[0]
+    if M == 0:
+        return
+    dev = x.device
+    lib = _lib.load()
+    with _on_device(dev):
+        wsb = _lib.check(lib.awq_gated_mlp_workspace_bytes(M, H, I, G, dtype_code(x.dtype)),
+                         "awq_gated_mlp_workspace_bytes")
+        ws = _workspace(wsb, dev)
+        _lib.check(lib.awq_gated_mlp(x.data_ptr(), gw.data_ptr(), gs.data_ptr(), gz.data_ptr(), dw.data_ptr(),
+                                     ds.data_ptr(), dz.data_ptr(), out.data_ptr(), M, H, I, G, dtype_code(x.dtype),
+                                     _GATED_ACT[activation], polls, _ptr(ws), wsb, counters.data_ptr(),
+                                     counters.numel() * 4, _stream(dev)), "awq_gated_mlp")
+
+
+@torch.library.custom_op(f"{NAMESPACE}::awq_gated_mlp_out", mutates_args=("counters", "out"), device_types="cuda")
+def _mlp_out_op(x: torch.Tensor, gw: torch.Tensor, gs: torch.Tensor, gz: torch.Tensor, dw: torch.Tensor,
+                ds: torch.Tensor, dz: torch.Tensor, counters: torch.Tensor, out: torch.Tensor, H: int, I: int, G: int,
+                activation: str, polls: int) -> None:
+    _mlp_launch(x, gw, gs, gz, dw, ds, dz, counters, out, H, I, G, activation, polls)
+
+
+@_mlp_out_op.register_fake
+def _(x, gw, gs, gz, dw, ds, dz, counters, out, H, I, G, activation, polls):
+    return None
+
+
+def gated_mlp(x: torch.Tensor, gate_up: Repacked, down: Repacked, H: int, I: int, group_size: int,
+              counters: torch.Tensor, activation: str = "silu", out: Optional[torch.Tensor] = None,
+              polls: Optional[int] = None) -> torch.Tensor:
+    """out[M, H] = down(act(gate) * up) of a gated MLP block in one launch (awq_gated_mlp).
+
+    ``gate_up`` is the merged projection repacked as K = H, N = 2I (gate columns first), ``down`` the
+    down projection as K = I, N = H; group size 128, no bias.  The gate and up values are rounded and
+    combined exactly as ``gemm(..., activation=...)`` stores them, and the down projection's k-slice
+    sums are added in a fixed order.  ``counters`` from ``make_mlp_counters``.  ``polls`` bounds each
+    workgroup's wait for its k-slice of the intermediate (None: the library default); a workgroup
+    that gives up makes the call's output invalid and is reported by ``mlp_check``.  Raises RuntimeError when
+    ``gated_mlp_plan`` has no plan for the shape."""
+    _require_cuda(x, gate_up.w, down.w, counters)
+    if x.dim() != 2 or x.shape[1] != H:
+        raise ValueError(f"x must be [M, {H}], got {tuple(x.shape)}")
+    if x.dtype != gate_up.s.dtype or x.dtype != down.s.dtype:
+        raise ValueError(f"activation dtype {x.dtype} does not match the scale dtypes")
+    if activation not in _GATED_ACT:
+        raise ValueError(f"unsupported activation {activation!r}")
+    dev = x.device
+    for t in (gate_up.w, gate_up.s, gate_up.z, down.w, down.s, down.z):
+        if t.device != dev:
+            raise ValueError("x and the repacked weights must be on one device")
+    if counters.dtype != torch.int32 or counters.device != dev or not counters.is_contiguous() \
+            or counters.numel() * 4 < _lib.AWQ_MLP_COUNTER_BYTES or counters.data_ptr() % 128:
+        raise ValueError("counters must be make_mlp_counters(device)")
+    G = resolve_group_size(group_size, H)
+    M = x.shape[0]
+    x = _aligned(x)
+    if out is None:
+        out = torch.empty((M, H), dtype=x.dtype, device=dev)
+    else:
+        _check_out(out, (M, H), x.dtype, dev)
+    torch.ops.sglite_awq.awq_gated_mlp_out(x, gate_up.w, gate_up.s, gate_up.z, down.w, down.s, down.z, counters,
+                                           out, H, I, G, activation, -1 if polls is None else int(polls))
+    return out
+
+
 def stream_probe(src: torch.Tensor, nbytes: int, grid: int, block: int, sink: torch.Tensor) -> None:
     """Stream ``nbytes`` of ``src`` with ``grid`` workgroups of ``block`` threads (awq_stream_probe)."""
     _require_cuda(src, sink)

@@ -200,8 +200,8 @@ def test_short_counters_are_reported_before_launch():
 
 def test_abi_version_and_counter_layout():
     lib = _lib.load()
-    assert lib.awq_abi_version() == _lib.AWQ_ABI_VERSION == 3
-    assert lib.awq_version().decode().endswith("0.3")
+    assert lib.awq_abi_version() == _lib.AWQ_ABI_VERSION == 4
+    assert lib.awq_version().decode().endswith("0.4")
     # the constants the binding mirrors agree with the library's sizes
     assert lib.awq_counter_bytes(16) == _lib.AWQ_COUNTER_TILE_BYTES + 4
     assert lib.awq_counter_bytes(_lib.AWQ_NOALLOC_MAX_N) == _lib.AWQ_COUNTER_TILE_BYTES + _lib.AWQ_NOALLOC_MAX_N // 4
@@ -209,7 +209,7 @@ def test_abi_version_and_counter_layout():
     import ctypes
     saved = _lib.AWQ_ABI_VERSION
     try:
-        _lib.AWQ_ABI_VERSION = 2
+        _lib.AWQ_ABI_VERSION = 3
         with pytest.raises(RuntimeError, match="ABI"):
             _lib._lib, keep = None, _lib._lib
             try:
@@ -365,6 +365,42 @@ def test_fused_activation_entry_validates_before_launch():
     assert need > 0
     st = lib.awq_w4a16_gemm_act(*args, M, N, K, 128, 0, _lib.AWQ_ACT_SILU, None, 0, None, 0, None)
     assert st == _lib.AWQ_STATUS_WORKSPACE
+
+
+def test_gated_mlp_entry_validates_before_launch():
+    lib = _lib.load()
+    fake = 0x10000  # never dereferenced: validation fails first
+    # workspace: the intermediate [M, I] (256-byte rounded), then 1..256 fp32 [M, H] partials
+    for M, H, I in [(1, 2560, 9728), (8, 2560, 9728), (16, 4096, 14336), (3, 512, 768)]:
+        b = lib.awq_gated_mlp_workspace_bytes(M, H, I, 128, 0)
+        hb = (M * I * 2 + 255) // 256 * 256
+        assert b > hb and (b - hb) % (M * H * 4) == 0 and 1 <= (b - hb) // (M * H * 4) <= 256, (M, H, I, b)
+    # outside the built forms: more rows, a wider hidden size, another group size
+    for M, H, I, G in [(17, 2560, 9728, 128), (1, 8192, 3584, 128), (1, 2560, 9728, 64)]:
+        assert lib.awq_gated_mlp_workspace_bytes(M, H, I, G, 0) == _lib.AWQ_STATUS_UNSUPPORTED
+    assert lib.awq_gated_mlp_workspace_bytes(1, 2560, 9727, 128, 0) == -1  # 2I columns not packable
+    w = (fake,) * 7
+    M, H, I = 4, 2560, 9728
+    need = lib.awq_gated_mlp_workspace_bytes(M, H, I, 128, 0)
+    cb = _lib.AWQ_MLP_COUNTER_BYTES
+
+    def call(*, x=fake, act=_lib.AWQ_ACT_SILU, m=M, ws=fake, wsb=need, cnt=fake, cntb=cb, h=H, g=128):
+        return lib.awq_gated_mlp(x, *w, m, h, I, g, 0, act, -1, ws, wsb, cnt, cntb, None)
+
+    assert call(act=3) == -1 and "activation" in _lib.last_error()
+    assert call(x=None) == -1 and "null" in _lib.last_error()
+    assert call(x=fake + 8) == -1 and "aligned" in _lib.last_error()
+    assert call(m=17) == _lib.AWQ_STATUS_UNSUPPORTED and "built forms" in _lib.last_error()
+    assert call(g=64) == _lib.AWQ_STATUS_UNSUPPORTED
+    assert call(ws=None) == _lib.AWQ_STATUS_WORKSPACE and "workspace" in _lib.last_error()
+    assert call(wsb=need - 1) == _lib.AWQ_STATUS_WORKSPACE
+    assert call(ws=fake + 16) == _lib.AWQ_STATUS_WORKSPACE and "256-byte" in _lib.last_error()
+    assert call(cnt=None) == _lib.AWQ_STATUS_WORKSPACE and "counters" in _lib.last_error()
+    assert call(cntb=cb - 4) == _lib.AWQ_STATUS_WORKSPACE
+    assert call(cnt=fake + 64) == _lib.AWQ_STATUS_WORKSPACE and "128-byte" in _lib.last_error()
+    assert call(m=0, x=None) == 0
+    assert lib.awq_gated_mlp_take_errors(None, cb, None) == -1
+    assert lib.awq_gated_mlp_take_errors(fake, cb - 4, None) == -1
 
 
 def test_m_zero_is_a_noop():

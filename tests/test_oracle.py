@@ -436,3 +436,62 @@ def test_golden_fixtures_reproduce():
                 x = _half(g[key], dt)
                 y = oracle.awq_gemm(x, qw, qz, s, bias, G)
                 np.testing.assert_array_equal(y.view(torch.int16).numpy().view(np.uint16), g[f"{name}/y{M}"])
+
+
+def _dense_gated_mlp(x, tgu, tdn, G, act):
+    """The package's GatedMLP on the unquantized method with the dequantized weights."""
+    from sglite_amd.mlp import GatedMLP
+
+    H, I = x.shape[1], tdn["qweight"].shape[0]
+    mlp = GatedMLP(H, I, act)
+    wgu = oracle.dequantize(tgu["qweight"], tgu["qzeros"], tgu["scales"], G).float()
+    wdn = oracle.dequantize(tdn["qweight"], tdn["qzeros"], tdn["scales"], G).float()
+    mlp.load_state_dict({"gate_up_proj.weight": wgu.t().contiguous(), "down_proj.weight": wdn.t().contiguous()})
+    return mlp(x)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_gated_mlp_oracle_matches_dense_block_in_fp32(act):
+    """With fp32 activations no rounding separates the steps, so the oracle's composition must be
+    the dense block (blocks.py:51-57) on the same weights: gate half first, act on the gate only,
+    times up, then the down projection."""
+    H, I, G, M = 256, 384, 128, 5
+    tgu = oracle.make_awq_linear(H, 2 * I, G, seed=41)
+    tdn = oracle.make_awq_linear(I, H, G, seed=42)
+    x = oracle.make_activation(M, H, seed=43).float()
+    got = oracle.gated_mlp_awq(x, tgu, tdn, G, act)
+    ref = _dense_gated_mlp(x, tgu, tdn, G, act)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4 * float(ref.abs().max()))
+
+
+def test_gated_mlp_oracle_is_the_two_awq_gemms():
+    """At fp16 each of the oracle's GEMMs is awq_gemm itself (no bias), with the activation's
+    rounding in between."""
+    H, I, G, M = 256, 384, 64, 3
+    tgu = oracle.make_awq_linear(H, 2 * I, G, seed=47)
+    tdn = oracle.make_awq_linear(I, H, G, seed=48)
+    x = oracle.make_activation(M, H, seed=49)
+    y = oracle.awq_gemm(x, tgu["qweight"], tgu["qzeros"], tgu["scales"], None, G)
+    h = oracle.gelu_and_mul(y).to(torch.float16)
+    ref = oracle.awq_gemm(h, tdn["qweight"], tdn["qzeros"], tdn["scales"], None, G)
+    assert torch.equal(oracle.gated_mlp_awq(x, tgu, tdn, G, "gelu"), ref)
+
+
+def test_gated_mlp_oracle_rounds_between_steps_and_a_swapped_half_fails():
+    """At fp16 the oracle rounds the gate/up output, then act(gate) * up once, and the result stays
+    within fp16 error of the fp32 block; a gate/up swap (a plausible slip) is caught by the same
+    tolerance rule the GPU tests use."""
+    H, I, G, M = 256, 384, 128, 4
+    tgu = oracle.make_awq_linear(H, 2 * I, G, seed=44)
+    tdn = oracle.make_awq_linear(I, H, G, seed=45)
+    x = oracle.make_activation(M, H, seed=46)
+    got = oracle.gated_mlp_awq(x, tgu, tdn, G, "silu")
+    assert got.dtype == torch.float16 and got.shape == (M, H)
+    ref = _dense_gated_mlp(x.float(), tgu, tdn, G, "silu")
+    ok, err, mx = oracle.tolerance_ok(got, ref, 2e-2)
+    assert ok, (err, mx)
+    y = oracle.awq_gemm(x, tgu["qweight"], tgu["qzeros"], tgu["scales"], None, G)
+    swapped = torch.cat([y[:, I:], y[:, :I]], dim=1)
+    h_bad = oracle.silu_and_mul(swapped).to(torch.float16)
+    bad = oracle.awq_gemm(h_bad, tdn["qweight"], tdn["qzeros"], tdn["scales"], None, G)
+    assert not oracle.tolerance_ok(bad, ref, 2e-2)[0]
