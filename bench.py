@@ -1115,6 +1115,68 @@ def hipblaslt_bench(ops, dev, reps: int = 15) -> dict:
     return out
 
 
+# Planner check on shapes it was not tuned on: one GPU's share of tensor-
+# parallel linears, beside the Qwen3-4B and Llama-3-8B configuration shapes.
+# Every other built kernel form is forced through the planner overrides and
+# timed the same way (graph replay over rotating weight copies, best of two
+# rounds); a case passes when the planner's plan is within 5% of the fastest.
+SWEEP_GROUPS = {"qwen3_4b": LAYER, "llama3_8b": PREFILL, **TP_SHARDS}
+_FORCE_TILED = 99999
+
+
+def _sweep_forms(M: int) -> list:
+    if M > 32:
+        return [{"tiled_min_m": 1, "tiled_bm": c} for c in (64, 128, 1064, 1128, 2064, 2128, 8064, 8128, 9064, 9128)]
+    forms = [{"tiled_min_m": _FORCE_TILED, "gemv_max_m": 32, "gemv_variant": v}
+             for v in (11083, 11084, 11086, 11088, 11165, 11168, 12083, 12084, 15037, 21083, 23054)]
+    forms += [{"tiled_min_m": _FORCE_TILED, "gemv_max_m": 0, "skinny_variant": v}
+              for v in (10104, 10108, 10116, 10202, 10401, 10404, 20202, 20401, 20204)]
+    forms += [{"kslice_variant": v} for v in (142, 141, 222, 412)]
+    forms += [{"tiled_min_m": 1, "tiled_bm": c} for c in (32, 4032, 64, 1064)]
+    return forms
+
+
+def planner_sweep(ops, dev, groups, Ms) -> None:
+    gen = torch.Generator(device=dev).manual_seed(0)
+    print("| shapes | layer | K x N | M | planner's plan | us | fastest form | us | ratio |", flush=True)
+    print("|---|---|---|---|---|---|---|---|---|", flush=True)
+    for grp in groups:
+        for name, K, N in SWEEP_GROUPS[grp]:
+            for M in Ms:
+                C = 3 if M >= 1024 else 8
+                reps = [make_repacked(ops, K, N, gen, dev) for _ in range(C)]
+                cnt = ops.make_counters(N, dev)
+                x = torch.randn((M, K), generator=gen, device=dev).to(torch.float16)
+                out = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+                def timed():
+                    f = lambda: [ops.gemm(x, r, K, N, G, counters=cnt, out=out) for r in reps]  # noqa: E731
+                    for _ in range(2):
+                        f()
+                    g = graph_of(f)
+                    time_replays([g], 2)
+                    return median(replay_samples([g], 15 if M >= 1024 else 30)) * 1e3 / C
+
+                best = {}
+                default = None
+                for _ in range(2):
+                    for ov in [None] + _sweep_forms(M):
+                        ops.clear_plan_overrides()
+                        for k, v in (ov or {}).items():
+                            ops.set_plan_override(k, v)
+                        i = ops.plan_info(M, N, K, G)
+                        key = f"{i.function} {i.variant} ks{i.k_slices} {i.workgroups}x{i.threads}"
+                        if ov is None:
+                            default = key
+                        best[key] = min(best.get(key, float("inf")), timed())
+                ops.clear_plan_overrides()
+                fk = min(best, key=best.get)
+                print(f"| {grp} | {name} | {K} x {N} | {M} | {default} | {best[default]:.2f} | {fk} | "
+                      f"{best[fk]:.2f} | {best[default] / best[fk]:.3f} |", flush=True)
+                del reps
+                torch.cuda.empty_cache()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1126,6 +1188,9 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-mlp", action="store_true", help="skip the fused/unfused gated MLP block comparison")
     ap.add_argument("--no-stack", action="store_true", help="skip the 70B-shaped stack (35.6 GB of weights)")
+    ap.add_argument("--planner-sweep", nargs=2, metavar=("GROUPS", "MS"),
+                    help="time the planner's plan against every other built form on shape groups (comma list of "
+                         + ", ".join(SWEEP_GROUPS) + ") at batch sizes MS (comma list); print a markdown table")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the tensor-parallel shard, bf16 and hipBLASLt comparison sections")
     ap.add_argument("--no-decode", action="store_true",
@@ -1171,6 +1236,9 @@ def main() -> int:
     gen = torch.Generator(device=dev).manual_seed(0)
     if args.pmc_workload:
         return pmc_workload(ops, dev, gen)
+    if args.planner_sweep:
+        planner_sweep(ops, dev, args.planner_sweep[0].split(","), [int(m) for m in args.planner_sweep[1].split(",")])
+        return 0
     if args.profile_workload:
         profile_workload(args.profile_workload, ops, dev, gen)
         return 0

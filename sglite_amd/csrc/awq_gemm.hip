@@ -161,7 +161,10 @@ int gemv_default_variant(const Geom& g, int act) {
     for (int v : {11084, 11086, 11088, 11165, 11166, 11168})
       if (((v / 10) % 100) * (v % 10) >= g.KT) return v;
   }
-  const int wn = g.M >= (g.NT >= 1024 ? 7 : 5) ? 2 : 1;
+  // Two column tiles per workgroup only where that still leaves >= 192
+  // workgroups (tensor-parallel shards at M = 8: a 1280-column qkv shard, 80
+  // tiles, 9.7 -> 9.1 us with one tile per workgroup).
+  const int wn = g.M >= (g.NT >= 1024 ? 7 : 5) && g.NT >= 384 ? 2 : 1;
   const int v3 = 10083 + wn * 1000, v4 = v3 + 1;
   const int64_t k3 = gemv_split(g, v3, gemv_min_ks(g, v3)).ks, k4 = gemv_split(g, v4, gemv_min_ks(g, v4)).ks;
   return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? v3 : v4;
@@ -183,8 +186,20 @@ bool gemv_preferred(const Geom& g, int act) {
   const int forced = knob(kPlanGemvMaxM, -1);
   if (forced >= 0) return g.M <= forced;
   if (act) return g.M <= 4 || (g.M <= 8 && g.KT <= 24);
+  // K of at most 8 k-tiles (tensor-parallel o_proj shards): the GEMV
+  // kernel's staged activation slice costs more than the skinny kernel's
+  // per-wave fragments up to 16 rows (1024 x 8192 at M = 1: 5.2 -> 4.7 us;
+  // 1024 x 4096 at M = 8: 5.0 -> 4.5 us); at 17-32 rows on wide layers the
+  // GEMV kernel's two-tile workgroups win (1024 x 8192 at M = 32: 7.6 -> 6.7 us).
+  if (g.KT <= 8) return g.M > 16 && g.NT >= 384;
   if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
   if (g.M > 16) return false;
+  // Fewer than 128 column tiles: the skinny kernel would split K to fill the
+  // CUs (4096 x 1536 at M = 8: 9.0 -> 6.8 us on the GEMV kernel, K unsplit);
+  // narrow layers with short K (at most 16 k-tiles) keep the skinny kernel
+  // (2048 x 4096 at M = 8: 5.8 -> 5.2 us).
+  if (g.NT < 128) return true;
+  if (g.KT <= 16 && g.NT <= 256) return false;
   if (g.KT <= 24) return true;
   if (g.NT >= 1024 || (g.NT < 384 && g.KT < 64)) return false;
   const int v = gemv_default_variant(g, 0);
@@ -294,15 +309,27 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // wide layers (>= 1024 column tiles) use two column tiles per wave;
     // narrower ones put one column tile per workgroup and split K over 4-16
     // waves, more of them for short or very long K.
+    // Short K (at most 8 k-tiles) at up to 16 rows: two column tiles per
+    // workgroup in two waves each where that still gives one workgroup per
+    // CU, else 16 waves on one tile; at 17-32 rows on narrow layers with up
+    // to 16 k-tiles, 4 waves (1024 x 4096 at M = 32: 5.9 -> 5.4 us).  Narrow
+    // layers with 25-31 or 48-63 k-tiles take 16 waves as the shorter and
+    // longer ones do (3584 x 4096 at M = 8: 7.5 -> 6.6 us; 7168 x 4096:
+    // 11.4 -> 9.7 us).
     int ntw = 1, wn = 1, wk = 4;
     if (g.NT >= 1024) {
       ntw = 2;
       wn = g.M <= 8 ? 2 : 4;
       wk = g.M <= 8 ? 2 : 1;
+    } else if (g.KT <= 8 && g.M <= 16) {
+      wn = g.NT >= 2 * g.cus ? 2 : 1;
+      wk = wn == 2 ? 2 : 16;
     } else if (g.M > 16 && g.NT >= 384) {
       wn = 2;
       wk = 2;
-    } else if (g.KT <= 24 || g.KT >= 64) {
+    } else if (g.M > 16 && g.KT <= 16) {
+      wk = 4;
+    } else if (g.KT < 32 || g.KT >= 48) {
       wk = 16;
     } else {
       wk = g.M <= 8 ? 4 : (g.M <= 16 ? 8 : 16);
@@ -372,7 +399,8 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     int best_bm = 0, best_ks = 1;
     for (int code : {32, 64, 128, 1064, 1128, 2064, 2128, 4032, 8064, 8128, 9064, 9128}) {
       const int bm = code % 1000;
-      if (env_bm_ok ? code != env_bm : code >= 1000) continue;  // the 32x32 kernel only on request (for now)
+      // the cost model ranks the 16x16 codes; the rules below move shapes to the 32x32 forms
+      if (env_bm_ok ? code != env_bm : code >= 1000) continue;
       if (g.K > tiled_max_k(bm) || (!env_bm_ok && bm == 32 && !bm32_ok)) continue;
       const int64_t tiles = ((g.NT + 15) / 16) * ((g.M + bm - 1) / bm);
       const int64_t min_ktc = g.M <= 32 ? 2 : 4;  // k-tiles per slice at least
@@ -465,7 +493,11 @@ GemmPlan plan_gemm(const Geom& g, int act) {
       }
     }
     const int64_t t2_128 = ((g.NT + 15) / 16) * ((g.M + 127) / 128);
-    if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 192 && 2 * t2_128 > g.cus && t2_128 <= g.cus) {
+    // (With K of fewer than 16 k-tiles the split leaves too few k-steps per
+    // wave: a 1024 x 4096 o_proj shard at M = 2048 runs 28.8 us there and
+    // 27.0 us in the two-workgroup form.)
+    if (!env_bm_ok && best_bm == 128 && g.G >= 64 && g.M > 192 && g.KT >= 16 && 2 * t2_128 > g.cus &&
+        t2_128 <= g.cus) {
       best_bm = 9128;
       ks = 1;
     }
@@ -476,7 +508,7 @@ GemmPlan plan_gemm(const Geom& g, int act) {
       if (2 * t2 >= 3 * cus) {
         best_bm = 2128;
         if (g.G >= 128 && (t8 <= cus || t8 % cus == 0 || 4 * (t8 % cus) >= 3 * cus)) best_bm = 8128;
-      } else if (g.M > 256 && t2 < cus) {
+      } else if (g.M > 256 && (t2 < cus || (g.KT < 16 && t2 <= cus))) {
         best_bm = 2128;
       } else if (g.M > 256 && g.G >= 128 && t2 > cus && t8 <= cus) {
         best_bm = 8128;
@@ -497,10 +529,12 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // 77.4 / 88.3 -> 80.6 us against the two-workgroup form), else the two-
     // workgroup form (code 2064: Qwen3-4B gate_up at M = 128 30.5 -> 28.2 us
     // against the 16x16 kernel, 1-8% faster in every case measured).
-    if (!env_bm_ok && ks == 1 && g.G >= 128 && g.M <= 256) {
+    // A 64-row block takes the 32x32 kernel at larger M too (a 4096 x 1536
+    // qkv shard at M = 2048: 45.3 -> 37.6 us in the k-wave split).
+    if (!env_bm_ok && ks == 1 && g.G >= 128) {
       const int64_t t8 = ((g.NT + 31) / 32) * ((g.M + 63) / 64);
       const int64_t t64 = ((g.NT + 15) / 16) * ((g.M + 63) / 64);
-      if (best_bm == 128 && 4 * t8 <= 3 * (int64_t)g.cus) best_bm = 8064;
+      if (best_bm == 128 && g.M <= 256 && 4 * t8 <= 3 * (int64_t)g.cus) best_bm = 8064;
       else if (best_bm == 64) best_bm = t64 <= g.cus ? 9064 : 2064;
     }
     p.variant = best_bm;

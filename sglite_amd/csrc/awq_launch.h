@@ -26,7 +26,7 @@ enum : int {
   kPlanSkinnyVariant = 3, // decode-kernel shape code ntw*10000 + wn*100 + wk
   kPlanSkinnyKs = 4,      // decode-kernel k-slices
   kPlanTiledMinM = 5,     // smallest M routed to the tiled kernel
-  kPlanTiledBm = 6,       // tiled row block (32, 64, 128)
+  kPlanTiledBm = 6,       // tiled row-block code (32, 64, 128; 1064 ... 8128; 9064, 9128 with G >= 64)
   kPlanTiledKs = 7,       // tiled k-slices
   kPlanKsliceVariant = 8, // in-kernel split-K decode kernel shape wn*100 + wk*10 + kpw
   kPlanTiledFixup = 9,    // 0: tiled split-K plans sum their slices in a second kernel

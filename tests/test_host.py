@@ -133,11 +133,28 @@ def test_gemv_keeps_deep_k_unsplit_at_few_rows():
     assert ops.workspace_bytes(1, 8192, 28672, 128) > 0  # 224 k-tiles still split
 
 
+def test_tensor_parallel_shard_routing():
+    """Shapes the planner was not tuned on (one GPU's share of tensor-parallel
+    linears): short K goes to the skinny kernel up to 16 rows, very narrow
+    layers keep K unsplit on the GEMV kernel, and the GEMV kernel's two-tile
+    workgroups need at least 384 column tiles."""
+    assert ops.gemm_kernel(1, 8192, 1024, 128) == "skinny_kernel"   # 70B o_proj at TP8
+    assert ops.plan_info(1, 8192, 1024, 128).variant == 10202
+    assert ops.plan_info(8, 4096, 1024, 128).variant == 10116       # Llama-3-8B o_proj at TP4
+    assert ops.gemm_kernel(32, 8192, 1024, 128) == "gemv_kernel"
+    info = ops.plan_info(8, 1536, 4096, 128)                        # Llama-3-8B qkv at TP4
+    assert info.kernel == "gemv_kernel" and info.k_slices == 1
+    assert ops.plan_info(8, 1280, 8192, 128).variant == 11084       # 70B qkv at TP8: one tile per workgroup
+    assert ops.plan_info(8, 6144, 2560, 128).variant == 12083       # Qwen3-4B qkv keeps two
+    assert ops.plan_info(2048, 1536, 4096, 128).variant == 9064     # 64-row block on the 32x32 kernel
+    assert ops.plan_info(2048, 4096, 1024, 128).variant == 2128     # short K: no k-wave split
+
+
 def test_fused_activation_routing():
     """The fused gate/up GEMM keeps the GEMV kernel to 8 rows on short K and the
     skinny kernel beyond, while the plain GEMM takes the GEMV kernel to 16 rows."""
-    assert ops.gemm_kernel(12, 2080, 2048, 128) == "gemv_kernel"
-    assert ops.gemm_kernel(12, 2080, 2048, 128, activation="silu") == "skinny_kernel"
+    assert ops.gemm_kernel(12, 2080, 2560, 128) == "gemv_kernel"
+    assert ops.gemm_kernel(12, 2080, 2560, 128, activation="silu") == "skinny_kernel"
     assert ops.gemm_kernel(8, 19456, 2560, 128, activation="silu") == "gemv_kernel"
     assert ops.gemm_kernel(300, 1056, 1024, 128, activation="gelu") == "tiled_kernel"
     with pytest.raises(ValueError, match="N % 32"):
