@@ -127,7 +127,8 @@ int device_cu_count() {
 // GEMV variant (code ntw * 10000 + wn * 1000 + wk * 10 + kpw): 8 waves of at
 // most 3 or 4 k-tiles each, whichever splits K fewer times (3 on a tie: fewer
 // load slots re-read a wave's last tile).  At 1-3 rows a K of 25-128 k-tiles
-// (up to 6 rows for 65-80 k-tiles) goes to the smallest of 8 waves x 4, 6 or
+// (4 rows from 33 k-tiles: Llama-3-8B down at M = 4 13.5 -> 11.8 us; up to 6
+// rows for 65-80 k-tiles) goes to the smallest of 8 waves x 4, 6 or
 // 8 and 16 waves x 5, 6 or 8 k-tiles that covers it: a split costs a
 // cross-workgroup handoff (~1.7 us), more than the workgroups it adds save
 // (Qwen3-4B down 8.4 -> 7.5 us at M = 1, 9.9 -> 9.3 us at M = 6; Llama-3-8B
@@ -157,14 +158,15 @@ int gemv_default_variant(const Geom& g, int act) {
   // slice once instead of five times (12.2 -> 10.1 us at M = 8; at M = 1 and
   // on layers whose workgroup count misses 256 it is slower).
   if (g.M >= 2 && g.NT > 1024 && g.NT <= 1280 && g.KT <= 21) return 15037;
-  if (g.KT > 24 && g.KT <= 128 && (g.M <= 3 || (g.M <= 6 && g.KT > 64 && g.KT <= 80))) {
+  if (g.KT > 24 && g.KT <= 128 && (g.M <= 3 || (g.M == 4 && g.KT > 32) || (g.M <= 6 && g.KT > 64 && g.KT <= 80))) {
     for (int v : {11084, 11086, 11088, 11165, 11166, 11168})
       if (((v / 10) % 100) * (v % 10) >= g.KT) return v;
   }
   // Two column tiles per workgroup only where that still leaves >= 192
   // workgroups (tensor-parallel shards at M = 8: a 1280-column qkv shard, 80
-  // tiles, 9.7 -> 9.1 us with one tile per workgroup).
-  const int wn = g.M >= (g.NT >= 1024 ? 7 : 5) && g.NT >= 384 ? 2 : 1;
+  // tiles, 9.7 -> 9.1 us with one tile per workgroup), from 4 rows below 1024
+  // column tiles (4096 x 14336 at M = 4: 10.8 -> 9.7 us).
+  const int wn = g.M >= (g.NT >= 1024 ? 7 : 4) && g.NT >= 384 ? 2 : 1;
   const int v3 = 10083 + wn * 1000, v4 = v3 + 1;
   const int64_t k3 = gemv_split(g, v3, gemv_min_ks(g, v3)).ks, k4 = gemv_split(g, v4, gemv_min_ks(g, v4)).ks;
   return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? v3 : v4;
@@ -241,7 +243,7 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
 //    projections: 48.7 -> 36.4 us for the down projection at M = 8; the
 //    Llama-3-8B down, 14336 x 4096: 16.5 -> 13.8 us at M = 8 on the 32-row
 //    32x32 kernel with 16 k-slices);
-//  * 14-16 rows on gate_up-sized matrices (N >= 16384, K * N >= 20M).
+//  * 14-16 rows with K beyond 24 k-tiles, N >= 8192 and K * N >= 20M.
 // A fused gate/up activation uses the 17-32 and 14-16 row rules only.
 bool tiled_preferred(const Geom& g, int act) {
   const int forced = knob(kPlanTiledMinM, 0);
@@ -249,7 +251,11 @@ bool tiled_preferred(const Geom& g, int act) {
   if (g.M > 32) return true;
   const int64_t kn = g.K * g.N;
   if (g.M > 16) return kn >= 12000000 && (g.N >= 6144 || g.K >= 8192);
-  if (g.M >= 14 && g.N >= 16384 && kn >= 20000000) return true;
+  // (14-16 rows: K of at most 24 k-tiles stays on the GEMV kernel, whose
+  // five-tile workgroups stage the short activation slice once: the Qwen3-4B
+  // gate_up at M = 16 13.1 -> 11.0 us; deeper K goes tiled: 4096 x 14336
+  // 16.1 -> 13.9 us.)
+  if (g.M >= 14 && g.KT > 24 && g.N >= 8192 && kn >= 20000000) return true;
   if (act) return false;
   if (g.M >= 10) return g.K >= 8192 && kn >= 40000000;
   return g.M >= 6 && g.K >= 8192 && g.N >= 4096 && g.N < 32768;

@@ -82,7 +82,7 @@ def test_workspace_query_is_bounded():
 @pytest.mark.parametrize("K,N,routes", [
     (2560, 6144, "g" * 16),                    # Qwen3-4B qkv: short K, GEMV throughout
     (4096, 2560, "g" * 4 + "s" * 12),          # Qwen3-4B o_proj: narrow, 32 k-tiles
-    (2560, 19456, "g" * 13 + "t" * 3),         # Qwen3-4B gate_up
+    (2560, 19456, "g" * 16),                   # Qwen3-4B gate_up: short K stays on the GEMV kernel
     (9728, 2560, "g" * 7 + "k" * 9),           # Qwen3-4B down: 76 k-tiles, k-slice kernel from 8 rows
     (4096, 6144, "g" * 16),                    # Llama-3-8B qkv
     (4096, 28672, "g" * 4 + "s" * 9 + "t" * 3),  # Llama-3-8B gate_up: wide
@@ -120,8 +120,8 @@ def test_kslice_routing_at_17_to_32_rows():
 
 def test_gemv_keeps_deep_k_unsplit_at_few_rows():
     """Up to 128 k-tiles one GEMV workgroup covers K at 1-3 rows (no split-K
-    workspace), and 65-80 k-tiles up to 6 rows; beyond that the 8-wave plans
-    split K again."""
+    workspace), 33-128 at 4 rows, and 65-80 k-tiles up to 6 rows; beyond that
+    the 8-wave plans split K again."""
     for K in (4224, 6144, 8192, 9728, 11008, 14336):
         for M in (1, 2, 3):
             assert ops.gemm_kernel(M, 4096, K, 128) == "gemv_kernel"
@@ -129,7 +129,8 @@ def test_gemv_keeps_deep_k_unsplit_at_few_rows():
     for M in (4, 5, 6):
         assert ops.workspace_bytes(M, 2560, 9728, 128) == 0, M
     assert ops.workspace_bytes(8, 2560, 9728, 128) > 0
-    assert ops.workspace_bytes(4, 4096, 14336, 128) > 0
+    assert ops.workspace_bytes(4, 4096, 14336, 128) == 0
+    assert ops.workspace_bytes(5, 4096, 14336, 128) > 0
     assert ops.workspace_bytes(1, 8192, 28672, 128) > 0  # 224 k-tiles still split
 
 
