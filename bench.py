@@ -591,7 +591,7 @@ def committed_traffic(kernel: str):
 # tiled kind runs tiled_kernel (16x16x32 MFMAs) or mfma32_kernel (32x32x16).
 DECODE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "kslice_kernel")
 TRACE_KERNELS = ("skinny_kernel", "gemv_kernel", "tiled_kernel", "mfma32_kernel", "splitk_reduce_kernel", "moe_",
-                 "topk_softmax_kernel", "align_kernel", "kslice_kernel")
+                 "topk_softmax_kernel", "align_kernel", "kslice_kernel", "mlp_kernel")
 
 
 def _trace_rows(trace_dir: str):
@@ -878,6 +878,12 @@ def rocprof_summary(trace_dir: str, command: str, section: str) -> str:
             f"* {n} dispatches over {passes} passes (the warm-up included): {ms:.2f} ms of kernel time per pass "
             f"= {byt / ms / 1e6:.1f} GB/s ({byt / ms / 1e6 / HBM_PEAK_GBS:.4f} of 8 TB/s) and "
             f"{fl / ms / 1e9:.1f} TFLOP/s ({fl / ms / 1e9 / MFMA_FP16_PEAK_TFLOPS:.4f} of 2.5 PFLOP/s)."]
+    elif section == "mlp":
+        lines = ["# Qwen3-4B gated MLP block (gate_up 2560x19456, silu, down 9728x2560) at M = 1, 8, 32, "
+                 "rocprofv3 kernel trace", ""] + head + [
+            "The bench's mlp section: each form replayed as HIP graphs over 12 weight copies -- the GEMMs with",
+            "the activation as torch ops, the activation in the gate_up GEMM's epilogue (two launches), and at",
+            "M <= 16 the whole block in one launch (`mlp_kernel`, 256 workgroups); int4 group 128, fp16."]
     else:
         lines = [f"# {section}, rocprofv3 kernel trace", ""] + head
     lines += [""] + _trace_table(groups)
