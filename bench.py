@@ -29,19 +29,19 @@ Also reported on the same line:
                 and bytes: what a launch of that shape reaches with no arithmetic.
   decode_kernels, per_m   the same per kernel and per batch size, with each
                 linear's probe ceiling (and the best ceiling over a few grids).
-  llama3_8b     config 2: Llama-3-8B's four linears at M = 1, 16, 256, 2048, 8192
+  llama3_8b     Llama-3-8B's four linears at M = 1, 16, 256, 2048, 8192
                 (GB/s and fraction of HBM at decode sizes, TFLOP/s and fraction of
                 the 2.5 PFLOP/s dense fp16 MFMA peak from M = 256);
   prefill       its M = 2048 aggregate (and M = 8192).
   mlp           the Qwen3-4B gated MLP with the activation fused vs unfused.
-  moe           config 4: the Qwen3-30B-A3B-shaped grouped MoE forward.
-  stack70b      config 3: the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at
+  moe           the Qwen3-30B-A3B-shaped grouped MoE forward.
+  stack70b      the Llama-3.1-70B-shaped 80-layer stack (35.6 GB) at
                 M = 64 (GB/s, one graph per pass) and M = 4096 (TFLOP/s).
   bounds        the MFMA-rate probe (awq_mfma_probe) at one and two waves per
                 SIMD: the compute bound the prefill TFLOP/s are read against.
-  cpu_baseline  the CPU oracle on the host cores for configs 0-4 (dequantisation
-                and matmul timed separately, 2 warm-ups, median of 5); value is
-                config 1 in GB/s.
+  cpu_baseline  the CPU oracle on the host cores for every workload above
+                (dequantisation and matmul timed separately, 2 warm-ups, median
+                of 5); value is the Qwen3-4B layer at M = 1, 8, 32 in GB/s.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 
@@ -374,14 +374,15 @@ def _host_cores() -> int:
 
 
 def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
-    """The CPU oracle on the host cores (BASELINE.md section 3): the oracle's torch dequantisation
+    """The CPU oracle on the host cores: the oracle's torch dequantisation
     (unpack in AWQ nibble order, (q - z) * s rounded once; pinned bit for bit against the numpy
     oracle) and fp32 matmul + cast, timed separately; `warmup` untimed runs, then the median of
-    `runs`.  Configs 0-2 in full except Llama-3-8B's M = 2048 and 8192, which time the o_proj
-    (4096x4096) alone; config 3 times one 70B-shaped o_proj (8192x8192) and scales it by the
-    layer's weight and flop counts (the full stack would need ~137 GB of fp16 weights); config 4
-    runs the expert loop over 16 of the 128 experts and scales by 8.  value = the headline
-    workload (config 1: Qwen3-4B layer at M = 1, 8, 32) in the metric's GB/s."""
+    `runs`.  The Qwen3-4B qkv at M = 16, the Qwen3-4B layer and Llama-3-8B's linears in full except
+    Llama-3-8B's M = 2048 and 8192, which time the o_proj (4096x4096) alone; the Llama-3.1-70B
+    stack times one 70B-shaped o_proj (8192x8192) and scales it by the layer's weight and flop
+    counts (the full stack would need ~137 GB of fp16 weights); the Qwen3-30B-A3B MoE runs the
+    expert loop over 16 of the 128 experts and scales by 8.  value = the headline workload (the
+    Qwen3-4B layer at M = 1, 8, 32) in the metric's GB/s."""
     from oracle import awq_oracle as oracle
 
     threads = _host_cores()
@@ -410,11 +411,11 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
         return td, tm
 
     res = {}
-    # config 0: Qwen3-4B qkv at M = 16
+    # Qwen3-4B qkv at M = 16
     td, tm = linear_times(2560, 6144, (16,), 0)
-    res["config0_qkv_m16"] = {"dequant_s": round(td, 4), "matmul_s": round(tm[16], 4),
+    res["qwen3_4b_qkv_m16"] = {"dequant_s": round(td, 4), "matmul_s": round(tm[16], 4),
                               "GB/s": round(gemm_bytes(16, 6144, 2560) / (td + tm[16]) / 1e9, 3)}
-    # config 1: the Qwen3-4B layer at M = 1, 8, 32 (the headline workload)
+    # the Qwen3-4B layer at M = 1, 8, 32 (the headline workload)
     step_b, step_t, deq_t, mm_t = 0, 0.0, 0.0, 0.0
     for i, (_, K, N) in enumerate(LAYER):
         td, tm = linear_times(K, N, M_SET, i)
@@ -423,10 +424,10 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
             step_t += td + tm[M]
             mm_t += tm[M]
         deq_t += td
-    res["config1_qwen3_4b_layer"] = {"dequant_s_per_layer": round(deq_t, 4), "matmul_s_per_step": round(mm_t, 4),
-                                     "GB/s": round(step_b / step_t / 1e9, 3)}
+    res["qwen3_4b_layer"] = {"dequant_s_per_layer": round(deq_t, 4), "matmul_s_per_step": round(mm_t, 4),
+                             "GB/s": round(step_b / step_t / 1e9, 3)}
     value = step_b / step_t / 1e9
-    # config 2: Llama-3-8B layer at M = 1, 16, 256 in full; 2048 and 8192 on the o_proj
+    # Llama-3-8B layer at M = 1, 16, 256 in full; 2048 and 8192 on the o_proj
     per_m = {M: [0, 0, 0.0] for M in LLAMA_M}
     for i, (name, K, N) in enumerate(PREFILL):
         Ms = [M for M in LLAMA_M if M <= 256 or name == "o_proj"]
@@ -435,9 +436,9 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
             per_m[M][0] += gemm_bytes(M, N, K)
             per_m[M][1] += 2 * M * N * K
             per_m[M][2] += td + tm[M]
-    res["config2_llama3_8b"] = {str(M): {"GB/s": round(b / t / 1e9, 3), "TFLOP/s": round(f / t / 1e12, 4)}
-                                for M, (b, f, t) in per_m.items()}
-    # config 3: one 70B-shaped o_proj, scaled to the 80-layer stack
+    res["llama3_8b"] = {str(M): {"GB/s": round(b / t / 1e9, 3), "TFLOP/s": round(f / t / 1e12, 4)}
+                        for M, (b, f, t) in per_m.items()}
+    # one 70B-shaped o_proj, scaled to the 80-layer stack
     K3, N3 = 8192, 8192
     td, tm = linear_times(K3, N3, (64, 4096), 20)
     w_layer = sum(K * N for _, K, N in STACK70B)
@@ -447,8 +448,8 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
         c3[str(M)] = {"s_per_stack_estimate": round(t_stack, 2),
                       "GB/s": round(80 * sum(gemm_bytes(M, N, K) for _, K, N in STACK70B) / t_stack / 1e9, 3),
                       "TFLOP/s": round(80 * sum(2 * M * N * K for _, K, N in STACK70B) / t_stack / 1e12, 4)}
-    res["config3_70b_stack"] = c3
-    # config 4: expert loop (gate_up 2048->1536 + silu_and_mul + down 768->2048), 16 of 128 experts
+    res["llama31_70b_stack"] = c3
+    # Qwen3-30B-A3B expert loop (gate_up 2048->1536 + silu_and_mul + down 768->2048), 16 of 128 experts
     E, Es, H, I, T, k = 128, 16, 2048, 768, 512, 8
     ex = [(oracle.make_awq_linear(H, 2 * I, G, seed=30 + e), oracle.make_awq_linear(I, H, G, seed=300 + e))
           for e in range(Es)]
@@ -464,7 +465,7 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
             (a @ W2).to(torch.float16)
     t4 = med(experts) * E / Es
     wb = E * (gemm_bytes(0, 2 * I, H) + gemm_bytes(0, H, I))
-    res["config4_moe"] = {"s_estimate": round(t4, 3), "GB/s": round((wb + T * k * (H + 2 * I + I + H) * 2) / t4 / 1e9, 3)}
+    res["qwen3_30b_a3b_moe"] = {"s_estimate": round(t4, 3), "GB/s": round((wb + T * k * (H + 2 * I + I + H) * 2) / t4 / 1e9, 3)}
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -477,9 +478,9 @@ def cpu_baseline(warmup: int = 2, runs: int = 5) -> dict:
     return {"value": round(value, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"CPU oracle (torch dequantise, pinned bit-exact to the numpy oracle, + fp32 matmul + fp16 "
                       f"cast), {warmup} warm-ups then the median of {runs}; value = the Qwen3-4B layer at M = 1, 8, "
-                      f"32 (config 1); other configs in per_config ({time.perf_counter() - t_start:.1f} s in all); "
+                      f"32; the other workloads in per_workload ({time.perf_counter() - t_start:.1f} s in all); "
                       f"host {model}, os.cpu_count() = {os.cpu_count()}",
-            "per_config": res}
+            "per_workload": res}
 
 
 PMC_COPY_BYTES = 256 << 20
@@ -985,7 +986,7 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
             "per_m": per_m}
 
 
-# Config 2's batches, the reference's graph-captured decode batches below 16
+# Llama-3-8B's batches, the reference's graph-captured decode batches below 16
 # (cuda_graph.py:76: [1, 2, 4] + multiples of 8), and the decode batches
 # 64..160 that graph capture covers.
 LLAMA_M = (1, 2, 4, 8, 16, 64, 128, 160, 256, 2048, 8192)
@@ -1056,7 +1057,7 @@ def linears_bench(ops, dev, prober, shapes, Ms, dtype=torch.float16, copies: int
 
 
 def llama_bench(ops, dev, gen, prober, copies: int = 10) -> dict:
-    """Config 2: Llama-3-8B's four linears at every M it names (1, 16, 256, 2048, 8192), at the
+    """Llama-3-8B's four linears at every M the workload names (1, 16, 256, 2048, 8192), at the
     graph-captured decode batches 2, 4, 8 and 64, 128, 160; int4 group 128, fp16."""
     res = linears_bench(ops, dev, prober, PREFILL, LLAMA_M, copies=copies)
     return {"workload": "Llama-3-8B AWQ linears (qkv 4096x6144, o 4096x4096, gate_up 4096x28672, down 14336x4096), "

@@ -233,7 +233,7 @@ def test_qwen3_4b_prefill_sizes(K, N, M):
 @pytest.mark.parametrize("K,N", LLAMA3_8B)
 @pytest.mark.parametrize("M", [1, 8, 16, 64, 96, 128, 160, 256, 1024, 2048, 8192])
 def test_llama3_8b_shapes(K, N, M):
-    """Config 2 at every M it names, up to the reference's largest prefill chunk
+    """Llama-3-8B's linears at every M the workload names, up to the reference's largest prefill chunk
     (max_extend_tokens = 8192, scheduler/config.py:20), and the decode batches
     64-160 that graph capture covers (cuda_graph.py:76)."""
     ops = _ops()
@@ -246,7 +246,7 @@ def test_llama3_8b_shapes(K, N, M):
     _check_full_size(y, W, x, t, K, N)
 
 
-def test_config0_qkv_against_cpu_oracle():
+def test_qwen3_4b_qkv_m16_against_cpu_oracle():
     """Qwen3-4B qkv_proj K=2560, N=6144, G=128, x [16, 2560], seed 0, checked on the CPU oracle."""
     y, ref, _ = _gemm_case(2560, 6144, 128, 16, seed=0)
     ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
