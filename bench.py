@@ -1127,7 +1127,7 @@ def hipblaslt_bench(ops, dev, reps: int = 15) -> dict:
 # Every other built kernel form is forced through the planner overrides and
 # timed the same way (graph replay over rotating weight copies, best of two
 # rounds); a case passes when the planner's plan is within 5% of the fastest.
-SWEEP_GROUPS = {"qwen3_4b": LAYER, "llama3_8b": PREFILL, **TP_SHARDS}
+SWEEP_GROUPS = {"qwen3_4b": LAYER, "llama3_8b": PREFILL, "llama31_70b": STACK70B, **TP_SHARDS}
 _FORCE_TILED = 99999
 
 

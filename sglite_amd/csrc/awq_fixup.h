@@ -8,15 +8,15 @@
 //
 //   1. the workgroup writes its partial with device-scope (write-through)
 //      stores and waits until they have completed;
-//   2. one thread adds 1 to the tile's arrival counter (device-scope atomic);
-//      arrival ks - 1 of this launch is the last;
+//   2. one thread adds 1 to the tile's arrival counter (agent-scope release,
+//      arrive_release); arrival ks - 1 of this launch is the last;
 //   3. every other workgroup polls the counter until all ks have arrived
-//      (bounded), marks its portion started and reduces it, reading the
-//      slices with system-scope loads (kCacheCoherentLoad); one that gives up
-//      simply exits;
-//   4. the last arrival reduces its own portion, then every portion that no
-//      workgroup has marked started (a portion reduced twice is stored twice
-//      with the same values), and advances the tile's base.
+//      (bounded), executes an agent-scope acquire (acquire_agent), marks its
+//      portion started and reduces it, reading the slices with system-scope
+//      loads (kCacheCoherentLoad); one that gives up simply exits;
+//   4. the last arrival acquires, reduces its own portion, then every portion
+//      that no workgroup has marked started (a portion reduced twice is
+//      stored twice with the same values), and advances the tile's base.
 //
 // So the result never depends on the workgroups being resident at the same
 // time -- the last arrival alone can finish every portion -- and a wait ends
@@ -129,13 +129,14 @@ __device__ __forceinline__ void splitk_fixup(const FixupTile<DT>& ft, uint32_t* 
   const uint32_t ks = (uint32_t)ft.ks;
   if (threadIdx.x == 0) {
     asm volatile("" ::"v"(base) : "memory");  // the base load has returned before this arrival
-    const uint32_t prev = __hip_atomic_fetch_add(tc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = arrive_release(tc);
     const bool last = prev - base == ks - 1u;
     bool ready = last;
     for (int i = 0; !ready && i < polls; ++i) {
       __builtin_amdgcn_s_sleep(2);
       ready = ld_sys_u32(tc) - base >= ks;
     }
+    if (ready) acquire_agent();  // the other slices' partials, before any wave loads them
     if (ready && !last) st_sys_u32(tc + 2 + kslice, base + 1u);
     s_fx[0] = last;
     s_fx[1] = ready;

@@ -1,6 +1,6 @@
 // W4A16 GEMM planning and dispatch for gfx950: out[M, N] = x[M, K] @ W
 // (+ bias), fp32 accumulation, optionally with the gated activation of a
-// merged gate/up projection fused (out[M, N / 2] = act(gate) * up).  Three
+// merged gate/up projection fused (out[M, N / 2] = act(gate) * up).  Four
 // kernels share the CDNA4 tile layout (awq_device.h):
 //
 //  * gemv_kernel (awq_gemv.hip): batches of a few rows, HBM-bound;
@@ -9,7 +9,8 @@
 //  * tiled_kernel (awq_tiled.hip): prefill (MFMA-bound) and 16-32 rows on
 //    large matrices, split K through a second reduction kernel;
 //  * kslice_kernel (awq_kslice.hip): decode batches up to 32 rows, split K
-//    reduced by the last workgroup of each column group.
+//    reduced by the last workgroup of each column group (planner override
+//    only).
 //
 // Replaces awq_gemm_kernel / awq_gemm_triton
 // (python/sglite/srt/model_executor/layers/quantization/awq_triton.py:16-195)
@@ -134,7 +135,7 @@ int device_cu_count() {
 // (Qwen3-4B down 8.4 -> 7.5 us at M = 1, 9.9 -> 9.3 us at M = 6; Llama-3-8B
 // down 12.2 -> 11.0 us and 70B-sized o 12.5 -> 10.9 us at M = 1; at 4 rows
 // and more on other depths the larger activation slices lose).  One column
-// tile per workgroup up to 4 rows; from 5 rows (7 on layers of >= 1024 column
+// tile per workgroup up to 4 rows; from 5 rows (7 on layers of >= 2048 column
 // tiles, where the workgroup count matters more) two column tiles share a
 // workgroup of 16 waves, which halves the activation slices staged per weight
 // byte.  With a fused gate/up activation a workgroup holds one gate tile and
@@ -157,6 +158,11 @@ int gemv_default_variant(const Geom& g, int act) {
   // k-tiles) put one workgroup on each CU, which then stages the activation
   // slice once instead of five times (12.2 -> 10.1 us at M = 8; at M = 1 and
   // on layers whose workgroup count misses 256 it is slower).
+  // From 14 rows on 1025-1536 column tiles with K within 20 k-tiles, six
+  // column tiles per workgroup (3 x 5 waves of 4 k-tiles, 203 workgroups on
+  // the Qwen3-4B gate_up) beat five: 11.8 -> 11.2 us at M = 16, and up to 24
+  // rows they beat the tiled kernel too (14.5 -> 13.2 us at M = 24).
+  if (g.M >= 14 && g.NT > 1024 && g.NT <= 1536 && g.KT <= 20) return 23054;
   if (g.M >= 2 && g.NT > 1024 && g.NT <= 1280 && g.KT <= 21) return 15037;
   if (g.KT > 24 && g.KT <= 128 && (g.M <= 3 || (g.M == 4 && g.KT > 32) || (g.M <= 6 && g.KT > 64 && g.KT <= 80))) {
     for (int v : {11084, 11086, 11088, 11165, 11166, 11168})
@@ -164,9 +170,10 @@ int gemv_default_variant(const Geom& g, int act) {
   }
   // Two column tiles per workgroup only where that still leaves >= 192
   // workgroups (tensor-parallel shards at M = 8: a 1280-column qkv shard, 80
-  // tiles, 9.7 -> 9.1 us with one tile per workgroup), from 4 rows below 1024
-  // column tiles (4096 x 14336 at M = 4: 10.8 -> 9.7 us).
-  const int wn = g.M >= (g.NT >= 1024 ? 7 : 4) && g.NT >= 384 ? 2 : 1;
+  // tiles, 9.7 -> 9.1 us with one tile per workgroup), from 4 rows below 2048
+  // column tiles (4096 x 14336 at M = 4: 10.8 -> 9.7 us; 4096 x 28672 at
+  // M = 6: 19.0 -> 18.2 us).
+  const int wn = g.M >= (g.NT >= 2048 ? 7 : 4) && g.NT >= 384 ? 2 : 1;
   const int v3 = 10083 + wn * 1000, v4 = v3 + 1;
   const int64_t k3 = gemv_split(g, v3, gemv_min_ks(g, v3)).ks, k4 = gemv_split(g, v4, gemv_min_ks(g, v4)).ks;
   return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? v3 : v4;
@@ -178,10 +185,11 @@ int gemv_default_variant(const Geom& g, int act) {
 //  * up to 4 rows, except 3-4 rows on very wide layers (>= 2048 column
 //    tiles: 5-10% slower than the skinny kernel's two-tile waves);
 //  * 5-16 rows, except on wide layers (>= 1024 column tiles) with K beyond
-//    24 k-tiles, narrow ones (< 384 column tiles) with K of 25-63 k-tiles, and
-//    wherever the activation slice would cut a workgroup's K range to 16
-//    k-tiles or fewer (2 per wave): there the workgroup's staged activation
-//    slice costs more than the skinny kernel's per-wave fragments.
+//    24 k-tiles other than at 7-8 rows, narrow ones (< 384 column tiles) with K of 25-63
+//    k-tiles, and wherever the activation slice would cut a workgroup's K
+//    range to 16 k-tiles or fewer (2 per wave): there the workgroup's staged
+//    activation slice costs more than the skinny kernel's per-wave fragments;
+//  * 17-24 rows with short K on layers of >= 384 column tiles (below).
 // A fused gate/up activation keeps the GEMV kernel up to 4 rows, and up to 8
 // rows when K fits in 24 k-tiles.
 bool gemv_preferred(const Geom& g, int act) {
@@ -195,15 +203,25 @@ bool gemv_preferred(const Geom& g, int act) {
   // GEMV kernel's two-tile workgroups win (1024 x 8192 at M = 32: 7.6 -> 6.7 us).
   if (g.KT <= 8) return g.M > 16 && g.NT >= 384;
   if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
-  if (g.M > 16) return false;
-  // Fewer than 128 column tiles: the skinny kernel would split K to fill the
-  // CUs (4096 x 1536 at M = 8: 9.0 -> 6.8 us on the GEMV kernel, K unsplit);
-  // narrow layers with short K (at most 16 k-tiles) keep the skinny kernel
-  // (2048 x 4096 at M = 8: 5.8 -> 5.2 us).
-  if (g.NT < 128) return true;
+  // 17-24 rows with K of 17-24 k-tiles on layers of >= 384 column tiles: the
+  // GEMV kernel's two-tile (or six-tile) workgroups stage the short
+  // activation slice once and beat the tiled kernel (Qwen3-4B qkv at M = 24:
+  // 11.1 -> 8.6 us); from 25 rows the tiled kernel wins.
+  if (g.M > 16) return g.M <= 24 && g.KT > 16 && g.KT <= 24 && g.NT >= 384;
+  // Fewer than 128 column tiles, up to 8 rows: the skinny kernel would split
+  // K to fill the CUs (4096 x 1536 at M = 8: 9.0 -> 6.8 us on the GEMV
+  // kernel, K unsplit); from 12 rows the skinny kernel's 16-wave workgroups
+  // win (7.4 against 8.4 us at M = 12).  Narrow layers with short K (at most
+  // 16 k-tiles) keep the skinny kernel (2048 x 4096 at M = 8: 5.8 -> 5.2 us).
+  if (g.NT < 128) return g.M <= 8;
   if (g.KT <= 16 && g.NT <= 256) return false;
   if (g.KT <= 24) return true;
-  if (g.NT >= 1024 || (g.NT < 384 && g.KT < 64)) return false;
+  // Wide layers with deep K: the skinny kernel's two-tile waves, except at
+  // 7-8 rows below 2048 column tiles, where the GEMV kernel's two-tile
+  // workgroups win (4096 x 28672
+  // at M = 7: 19.5 -> 18.3 us, at M = 8: 20.4 -> 18.8 us; at 5-6 rows the two
+  // are within run-to-run noise of each other).
+  if ((g.NT >= 1024 && (g.M <= 6 || g.M > 8 || g.NT >= 2048)) || (g.NT < 384 && g.KT < 64)) return false;
   const int v = gemv_default_variant(g, 0);
   return gemv_split(g, v, gemv_min_ks(g, v)).ktc > 16;
 }
@@ -230,35 +248,51 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
   return true;
 }
 
-// Batches of 6..32 rows: the tiled kernel (32-row block, K split up to 16
+// Batches of 5..32 rows: the tiled kernel (32-row block, K split up to 16
 // ways) beats both decode kernels on deep or wide matrices (graph replay of
-// the Qwen3-4B, Llama-3-8B and Llama-3-70B linears at M = 5..32 on MI355X):
+// the Qwen3-4B, Llama-3-8B, Llama-3-70B linears and their tensor-parallel
+// shards at M = 1..32 on MI355X):
 //  * 17-32 rows: K * N >= 12M with N >= 6144 or K >= 8192 (at M = 32 qkv,
 //    gate_up and down run 8-15% faster, e.g. 29.1 -> 24.7 us for a
 //    4096 x 28672 gate_up; the o_proj shapes stay 8-15% faster on the decode
-//    kernel);
+//    kernel), and the narrow deep layers below, except short K on wide
+//    layers up to 24 rows (the GEMV kernel's);
 //  * 10-16 rows: K >= 8192 and K * N >= 40M (14336 x 4096 down: 19.4 ->
 //    15.4 us at M = 16; 28672 x 8192 down: 67.7 -> 37.3 us);
-//  * 6-9 rows: K >= 8192 and 4096 <= N < 32768 (the 70B qkv, o and down
+//  * 5-9 rows: K >= 8192 and 4096 <= N < 32768 (the 70B qkv, o and down
 //    projections: 48.7 -> 36.4 us for the down projection at M = 8; the
-//    Llama-3-8B down, 14336 x 4096: 16.5 -> 13.8 us at M = 8 on the 32-row
-//    32x32 kernel with 16 k-slices);
-//  * 14-16 rows with K beyond 24 k-tiles, N >= 8192 and K * N >= 20M.
-// A fused gate/up activation uses the 17-32 and 14-16 row rules only.
+//    Llama-3-8B down, 14336 x 4096: 16.5 -> 13.8 us at M = 8 and 14.8 ->
+//    12.7 us at M = 5 on the 32-row 32x32 kernel with 16 k-slices);
+//  * 9-16 rows with >= 32 k-tiles, N >= 8192 and K * N >= 20M.
+// A fused gate/up activation uses the 17-32 and 9-16 row rules only.
 bool tiled_preferred(const Geom& g, int act) {
   const int forced = knob(kPlanTiledMinM, 0);
   if (forced > 0) return g.M >= forced;
   if (g.M > 32) return true;
   const int64_t kn = g.K * g.N;
-  if (g.M > 16) return kn >= 12000000 && (g.N >= 6144 || g.K >= 8192);
-  // (14-16 rows: K of at most 24 k-tiles stays on the GEMV kernel, whose
-  // five-tile workgroups stage the short activation slice once: the Qwen3-4B
-  // gate_up at M = 16 13.1 -> 11.0 us; deeper K goes tiled: 4096 x 14336
-  // 16.1 -> 13.9 us.)
-  if (g.M >= 14 && g.KT > 24 && g.N >= 8192 && kn >= 20000000) return true;
+  // Narrow layers with deep K (>= 48 k-tiles on <= 256 column tiles, or
+  // >= 32 k-tiles on < 128) split K 14-16 ways on the 32-row kernel from 17
+  // rows (Llama-3-8B down at TP2, 7168 x 4096, M = 24: 16.4 -> 12.7 us; the
+  // 70B qkv shard, 8192 x 1280: 13.7 -> 11.3 us; 4096 x 1536: 10.8 -> 9.5
+  // us), from 10 rows with >= 64 k-tiles (Qwen3-4B down at M = 12: 14.5 ->
+  // 11.3 us), and from 28 rows with >= 32 k-tiles (o_proj-shaped 4096 x 2560
+  // at M = 32: 12.1 -> 11.5 us).
+  const bool narrow_deep = (g.KT >= 48 && g.NT <= 256) || (g.KT >= 32 && g.NT < 128);
+  if (g.M > 16) {
+    if (g.M <= 24 && g.KT > 16 && g.KT <= 24 && g.NT >= 384) return false;  // the GEMV kernel's
+    return (kn >= 12000000 && (g.N >= 6144 || g.K >= 8192)) || narrow_deep || (g.M >= 28 && g.KT >= 32 && g.NT <= 256);
+  }
+  // (9-16 rows: K of at most 31 k-tiles stays on the GEMV kernel, whose
+  // workgroups stage the short activation slice once: the Qwen3-4B gate_up at
+  // M = 16 13.1 -> 11.0 us, the 70B down shard, 3584 x 8192, 10.7 -> 9.2 us;
+  // 32 and more k-tiles go tiled, where from 9 rows the GEMV kernel's
+  // activation slice takes 8 chunks per thread: 4096 x 14336 at M = 10 15.2
+  // -> 13.4 us, at M = 12 15.6 -> 13.5 us.)
+  if (g.M >= 9 && g.KT >= 32 && g.N >= 8192 && kn >= 20000000) return true;
   if (act) return false;
-  if (g.M >= 10) return g.K >= 8192 && kn >= 40000000;
-  return g.M >= 6 && g.K >= 8192 && g.N >= 4096 && g.N < 32768;
+  if (g.M >= 10)
+    return (g.K >= 8192 && kn >= 40000000) || (g.KT >= 64 && g.NT <= 256 && (g.NT >= 128 || g.M >= 12));
+  return g.M >= 5 && g.K >= 8192 && g.N >= 4096 && g.N < 32768;
 }
 
 // k-slice kernel plan of shape v (wn * 100 + wk * 10 + kpw): one k-slice of
@@ -282,30 +316,19 @@ bool plan_kslice(const Geom& g, int v, int act, GemmPlan& p) {
   return true;
 }
 
-// Where the k-slice kernel (64-column groups, 8 k-tiles per slice, the
-// reduction in the kernel) beats the other decode kernels, from a
-// graph-replay sweep of M = 8, 16, 32 over the Qwen3-4B and Llama-3-8B
-// projections on MI355X: narrow layers (<= 256 column tiles, one group per
-// k-tile) with 17-32 rows and 32-80 k-tiles (o_proj at M = 32: 11.8 ->
-// 10.7 us on Qwen3-4B, 12.1 -> 11.1 us on Llama-3-8B), and from 8 rows when K
-// spans 65-80 k-tiles (Qwen3-4B down: 11.1 -> 10.6, 12.7 -> 11.2 and
-// 14.4 -> 13.5 us at M = 8, 16, 32).  Deeper K (Llama-3-8B down, 112 k-tiles)
-// needs 14 slices and loses to the tiled kernel; wide layers and the fused
-// gate/up activation keep their kernels.
-bool kslice_preferred(const Geom& g, int act) {
-  if (act || g.M < 8 || g.M > 32 || g.NT > 256 || g.G < 128) return false;
-  if (g.KT > 64 && g.KT <= 80) return true;
-  return g.M > 16 && g.KT >= 32 && g.KT <= 80;
-}
+// The k-slice kernel is not chosen by the planner (only by the override):
+// its handoff of plain partial stores needs an agent-scope release (an L2
+// writeback) in every workgroup and an acquire in the last one, and with
+// them it loses to the other decode forms on every shape it used to win
+// (graph-replay sweep on MI355X, Qwen3-4B down 9728 x 2560: 12.96 us at M = 8
+// against 10.41 for the split GEMV, 15.61 at M = 32 against 13.48 for the
+// 16-slice 32-row tiled kernel; o_proj 4096 x 2560 at M = 32: 12.32 against
+// 11.59).
 
 GemmPlan plan_gemm(const Geom& g, int act) {
   GemmPlan p{};
   const int ksv = knob(kPlanKsliceVariant, 0);
   if (ksv != 0 && plan_kslice(g, ksv, act, p)) return p;
-  // A planner override of any other kernel keeps the k-slice kernel out.
-  const bool forced = knob(kPlanGemvMaxM, -1) >= 0 || knob(kPlanTiledMinM, 0) > 0 ||
-                      knob(kPlanSkinnyVariant, 0) != 0 || knob(kPlanGemvVariant, 0) != 0 || knob(kPlanTiledBm, 0) != 0;
-  if (!forced && ksv == 0 && kslice_preferred(g, act) && plan_kslice(g, 142, act, p)) return p;
   const bool tiled = tiled_preferred(g, act);
   if (!tiled && gemv_preferred(g, act) && plan_gemv(g, p, act)) return p;
   if (!tiled) {
@@ -317,11 +340,14 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     // waves, more of them for short or very long K.
     // Short K (at most 8 k-tiles) at up to 16 rows: two column tiles per
     // workgroup in two waves each where that still gives one workgroup per
-    // CU, else 16 waves on one tile; at 17-32 rows on narrow layers with up
-    // to 16 k-tiles, 4 waves (1024 x 4096 at M = 32: 5.9 -> 5.4 us).  Narrow
-    // layers with 25-31 or 48-63 k-tiles take 16 waves as the shorter and
-    // longer ones do (3584 x 4096 at M = 8: 7.5 -> 6.6 us; 7168 x 4096:
-    // 11.4 -> 9.7 us).
+    // CU, else 16 waves on one tile; otherwise narrow layers with up to 16
+    // k-tiles take 4 waves (1024 x 4096 at M = 32: 5.9 -> 5.4 us; 2048 x 4096
+    // at M = 8: 5.3 -> 5.0 us).  Narrow layers with 17-31 or 48-63 k-tiles
+    // take 16 waves (3584 x 4096 at M = 8: 7.5 -> 6.6 us; 7168 x 4096: 11.4 ->
+    // 9.7 us), 32-47 k-tiles 4 waves up to 8 rows and 8 beyond (4096 x 2560
+    // at M = 24: 10.6 -> 10.3 us), except on layers of fewer than 128 column
+    // tiles, where 16 waves keep K unsplit (4096 x 1536 at M = 10: 7.4 -> 7.0
+    // us).
     int ntw = 1, wn = 1, wk = 4;
     if (g.NT >= 1024) {
       ntw = 2;
@@ -333,12 +359,12 @@ GemmPlan plan_gemm(const Geom& g, int act) {
     } else if (g.M > 16 && g.NT >= 384) {
       wn = 2;
       wk = 2;
-    } else if (g.M > 16 && g.KT <= 16) {
+    } else if (g.KT <= 16) {
       wk = 4;
-    } else if (g.KT < 32 || g.KT >= 48) {
+    } else if (g.NT < 128 || g.KT < 32 || g.KT >= 48) {
       wk = 16;
     } else {
-      wk = g.M <= 8 ? 4 : (g.M <= 16 ? 8 : 16);
+      wk = g.M <= 8 ? 4 : 8;
     }
     if (act && ntw != 2) {  // a fused gate/up pair needs two tiles per wave
       ntw = 2;

@@ -21,14 +21,14 @@
 //
 // Split-K handoff: each workgroup writes its fp32 partial with device-scope
 // (SC1, write-through) 16-byte stores and waits until they have completed;
-// one thread then increments the column group's arrival counter (a
-// device-scope atomic).  The workgroup that sees the count reach ks - 1 reads
-// the ks partials back with system-scope loads (kCacheCoherentLoad), adds
-// them in slice order -- the same order whichever workgroup finishes last, so
-// results are deterministic -- stores the output (bias, fused gate/up
-// activation) and resets the counter for the next launch.  Every access that
-// crosses workgroups bypasses the caches it could find stale, so no
-// cache-wide writeback or invalidate is executed.
+// one thread then increments the column group's arrival counter with an
+// agent-scope release (arrive_release: an L2 writeback first).  The
+// workgroup that sees the count reach ks - 1 executes an agent-scope acquire
+// (acquire_agent: L1/L2 invalidate), reads the ks partials back with
+// system-scope loads (kCacheCoherentLoad), adds them in slice order -- the
+// same order whichever workgroup finishes last, so results are deterministic
+// -- stores the output (bias, fused gate/up activation) and resets the
+// counter for the next launch.
 //
 // Workgroup ids map XCD-aware onto (column group, k-slice): the workgroups one
 // XCD runs hold consecutive column groups of the same k-slice, so that XCD's
@@ -312,12 +312,14 @@ __global__ __launch_bounds__(256, 2) void kslice_kernel(KsArgs a) {
                                                  0, kCacheDevice);
       }
   }
-  // The partials are complete at device scope before the arrival is counted.
+  // The partials are complete before the arrival is counted (a release);
+  // the last arrival acquires before any of its waves loads them back.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&a.counters[bx], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = arrive_release(&a.counters[bx]);
     s_last = prev == a.ks - 1;
+    if (prev == a.ks - 1) acquire_agent();
   }
   __syncthreads();
   if (!s_last) return;

@@ -86,8 +86,9 @@ struct MlpArgs {
   int act, polls;
 };
 
-// Thread 0 arrives at a barrier slot and polls it until `n` arrivals since
-// `base` (at most `polls` polls); every thread gets the outcome.  The arrival
+// Thread 0 arrives at a barrier slot (an agent-scope release of this
+// workgroup's stores) and polls it until `n` arrivals since `base` (at most
+// `polls` polls), then acquires; every thread gets the outcome.  The arrival
 // that completes the count advances the base for the next launch.  A
 // workgroup that gives up adds one to the error word.
 __device__ __forceinline__ bool mlp_barrier(uint32_t* slot, uint32_t base, uint32_t n, int polls, uint32_t* err,
@@ -96,14 +97,17 @@ __device__ __forceinline__ bool mlp_barrier(uint32_t* slot, uint32_t base, uint3
   __syncthreads();
   if (threadIdx.x == 0) {
     asm volatile("" ::"v"(base) : "memory");  // the base was read before this arrival
-    const uint32_t prev = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = arrive_release(slot);
     bool ready = prev - base == n - 1u;
     if (ready) st_sys_u32(slot + 1, base + n);
     for (int i = 0; !ready && i < polls; ++i) {
       __builtin_amdgcn_s_sleep(1);
       ready = ld_sys_u32(slot) - base >= n;
     }
-    if (!ready) __hip_atomic_fetch_add(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ready)
+      acquire_agent();  // the others' stores, before any wave loads them
+    else
+      __hip_atomic_fetch_add(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_ok = ready;
   }
   __syncthreads();
@@ -361,9 +365,12 @@ __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs a) {
   __syncthreads();
   if (threadIdx.x == 0) {
     asm volatile("" ::"v"(baseg) : "memory");
-    const uint32_t prev = __hip_atomic_fetch_add(slotg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = arrive_release(slotg);
     const bool last = prev - baseg == (uint32_t)a.S - 1u;
-    if (last) st_sys_u32(slotg + 1, baseg + (uint32_t)a.S);
+    if (last) {
+      st_sys_u32(slotg + 1, baseg + (uint32_t)a.S);
+      acquire_agent();
+    }
     s_flag = last && ok;
   }
   __syncthreads();

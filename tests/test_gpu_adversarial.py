@@ -64,9 +64,10 @@ def test_gemv_biased_operand(M, dtype, kind):
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M", [4, 8, 16])
-def test_gemv_exact_integer_operand(M, dtype, kind):
-    """GEMV at 4-16 rows: fp16 takes the integers q - z, bf16 the dequantised weight."""
-    _run(M, 2560, 1024, dtype, kind, kernel="gemv_kernel")
+def test_gemv_exact_integer_operand(M, dtype, kind, plan):
+    """GEMV at 4-16 rows (forced: from 9 rows this 64-column-tile layer goes to the skinny
+    kernel): fp16 takes the integers q - z, bf16 the dequantised weight."""
+    _run(M, 2560, 1024, dtype, kind, plan=plan, knobs={"gemv_max_m": 16}, kernel="gemv_kernel")
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -74,7 +75,7 @@ def test_gemv_exact_integer_operand(M, dtype, kind):
 @pytest.mark.parametrize("M", [1, 9, 32])
 def test_skinny_biased_operand(M, dtype, kind, plan):
     """The skinny decode kernel (biased operand for every M), forced for every row count, split K."""
-    _run(M, 4096, 1024, dtype, kind, plan=plan, knobs={"gemv_max_m": 0}, kernel="skinny_kernel")
+    _run(M, 4096, 1024, dtype, kind, plan=plan, knobs={"gemv_max_m": 0, "tiled_min_m": 33}, kernel="skinny_kernel")
 
 
 @pytest.mark.parametrize("kind", ["mean10", "outliers"])
@@ -96,8 +97,8 @@ def test_tiled_dequant_path(dtype, kind):
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M", [8, 32])
-def test_kslice_dequant_path(M, dtype, kind):
+def test_kslice_dequant_path(M, dtype, kind, plan):
     """The k-slice decode kernel (bit-exact dequantisation into 32x32 MFMAs, the split-K
-    reduction in the kernel) on the Qwen3-4B down and o_proj shapes."""
+    reduction in the kernel; chosen by override only) on the Qwen3-4B down and o_proj shapes."""
     K, N = (9728, 2560) if M == 8 else (4096, 2560)
-    _run(M, K, N, dtype, kind, kernel="kslice_kernel")
+    _run(M, K, N, dtype, kind, plan=plan, knobs={"kslice_variant": 142}, kernel="kslice_kernel")

@@ -83,39 +83,50 @@ def test_workspace_query_is_bounded():
     (2560, 6144, "g" * 16),                    # Qwen3-4B qkv: short K, GEMV throughout
     (4096, 2560, "g" * 4 + "s" * 12),          # Qwen3-4B o_proj: narrow, 32 k-tiles
     (2560, 19456, "g" * 16),                   # Qwen3-4B gate_up: short K stays on the GEMV kernel
-    (9728, 2560, "g" * 7 + "k" * 9),           # Qwen3-4B down: 76 k-tiles, k-slice kernel from 8 rows
+    (9728, 2560, "g" * 9 + "t" * 7),           # Qwen3-4B down: 76 k-tiles on 160 column tiles, tiled from 10 rows
     (4096, 6144, "g" * 16),                    # Llama-3-8B qkv
-    (4096, 28672, "g" * 4 + "s" * 9 + "t" * 3),  # Llama-3-8B gate_up: wide
-    (14336, 4096, "g" * 5 + "t" * 11),         # Llama-3-8B down: deep, 32-row 32x32 kernel from 6 rows
-    (8192, 10240, "g" * 5 + "t" * 11),         # Llama-3-70B qkv
-    (8192, 57344, "gg" + "s" * 7 + "t" * 7),   # Llama-3-70B gate_up: very wide
-    (28672, 8192, "g" * 5 + "t" * 11),         # Llama-3-70B down
+    (4096, 28672, "g" * 4 + "ss" + "gg" + "t" * 8),  # Llama-3-8B gate_up: wide; two-tile GEMV at 7-8 rows
+    (14336, 4096, "g" * 4 + "t" * 12),         # Llama-3-8B down: deep, 32-row 32x32 kernel from 5 rows
+    (8192, 10240, "g" * 4 + "t" * 12),         # Llama-3-70B qkv
+    (8192, 57344, "gg" + "s" * 6 + "t" * 8),   # Llama-3-70B gate_up: very wide
+    (28672, 8192, "g" * 4 + "t" * 12),         # Llama-3-70B down
+    (4096, 1536, "g" * 8 + "s" * 8),           # Llama-3-8B qkv at TP4: < 128 column tiles
+    (8192, 1280, "g" * 8 + "sss" + "t" * 5),   # Llama-3-70B qkv at TP8: < 128 column tiles, 64 k-tiles
 ])
 def test_decode_routing(K, N, routes):
-    """Kernel choice for 1..16 rows (g = GEMV, s = skinny decode kernel, t = tiled, k = k-slice)."""
-    names = {"g": "gemv_kernel", "s": "skinny_kernel", "t": "tiled_kernel", "k": "kslice_kernel"}
+    """Kernel choice for 1..16 rows (g = GEMV, s = skinny decode kernel, t = tiled)."""
+    names = {"g": "gemv_kernel", "s": "skinny_kernel", "t": "tiled_kernel"}
     got = "".join(next(k for k, v in names.items() if v == ops.gemm_kernel(M, N, K, 128))
                   for M in range(1, len(routes) + 1))
     assert got == routes, (K, N)
 
 
-def test_kslice_routing_at_17_to_32_rows():
-    """Narrow layers with 32-80 k-tiles take the k-slice kernel from 17 rows
-    (o_proj), 65-80 k-tiles from 8 rows; deeper K, wide layers and the fused
-    activation keep their kernels."""
+def test_routing_at_17_to_32_rows():
+    """17-32 rows: short K on layers of >= 384 column tiles stays on the GEMV
+    kernel up to 24 rows; narrow layers with deep K (>= 48 k-tiles, or >= 32
+    on < 128 column tiles) split K on the 32-row tiled kernel; o_proj-shaped
+    layers (32 k-tiles, <= 256 column tiles) keep the skinny kernel up to 27
+    rows.  The planner never picks the k-slice kernel; the override does."""
+    for M in (17, 20, 24):
+        assert ops.gemm_kernel(M, 6144, 2560, 128) == "gemv_kernel"
+        assert ops.gemm_kernel(M, 19456, 2560, 128) == "gemv_kernel"
+        assert ops.gemm_kernel(M, 2560, 4096, 128) == "skinny_kernel"
+    for M in (25, 28, 32):
+        assert ops.gemm_kernel(M, 6144, 2560, 128) == "tiled_kernel"
+    for M in (28, 32):
+        assert ops.gemm_kernel(M, 2560, 4096, 128) == "tiled_kernel"
     for M in (17, 24, 32):
-        assert ops.gemm_kernel(M, 2560, 4096, 128) == "kslice_kernel"
-        assert ops.gemm_kernel(M, 4096, 4096, 128) == "kslice_kernel"
-        assert ops.gemm_kernel(M, 2560, 9728, 128) == "kslice_kernel"
-        assert ops.gemm_kernel(M, 4096, 14336, 128) != "kslice_kernel"  # 112 k-tiles
-        assert ops.gemm_kernel(M, 6144, 2560, 128) != "kslice_kernel"   # 384 column tiles
-        assert ops.gemm_kernel(M, 2560, 4096, 64) != "kslice_kernel"    # two groups per k-tile
-    assert ops.gemm_kernel(16, 2560, 4096, 128) != "kslice_kernel"
-    assert ops.gemm_kernel(8, 2560, 9728, 128) == "kslice_kernel"
-    assert ops.gemm_kernel(7, 2560, 9728, 128) != "kslice_kernel"
-    assert ops.gemm_kernel(32, 2 * 1280, 4096, 128, activation="silu") != "kslice_kernel"
-    info = ops.plan_info(32, 2560, 4096, 128)
-    assert info.variant == 142 and info.k_slices == 4 and info.workgroups == 160
+        assert ops.gemm_kernel(M, 2560, 9728, 128) == "tiled_kernel"  # 76 k-tiles
+        assert ops.gemm_kernel(M, 4096, 7168, 128) == "tiled_kernel"  # 56 k-tiles
+        assert ops.gemm_kernel(M, 1536, 4096, 128) == "tiled_kernel"  # 96 column tiles
+        assert ops.gemm_kernel(M, 4096, 3584, 128) == "skinny_kernel"  # 28 k-tiles
+    for M in range(1, 33):
+        for K, N in ((4096, 2560), (9728, 2560), (4096, 4096), (7168, 4096)):
+            assert ops.gemm_kernel(M, N, K, 128) != "kslice_kernel"
+    with ops.plan_overrides(kslice_variant=142):
+        info = ops.plan_info(32, 2560, 4096, 128)
+        assert info.kernel == "kslice_kernel" and info.variant == 142 and info.k_slices == 4
+        assert info.workgroups == 160
 
 
 def test_gemv_keeps_deep_k_unsplit_at_few_rows():
