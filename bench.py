@@ -17,8 +17,9 @@ linear moves K*N/2 (int4) + (K/128)*N/2 (zeros) + (K/128)*N*2 (scales)
 figure).  Every other duration is also a median of >= 50 samples.
 
 Also reported on the same line:
-  roofline      the dominant decode kernel of the step (the one with the most
-                time; ops.plan_info names the kernel of each shape): algorithmic
+  roofline      the dominant decode kernel of the step (the one that moves the
+                most of its algorithmic bytes; ops.plan_info names the kernel
+                of each shape): algorithmic
                 bytes of its launches / their durations, measured with HIP events
                 around graphs of back-to-back launches on the launch stream,
                 against 8 TB/s HBM; `traffic` is its HBM bytes per launch from
@@ -967,8 +968,11 @@ def decode_bench(ops, args, C, linear, step_fn, step_bytes, prober):
         per_m[str(M)] = {"GB/s": round(mb / mt / 1e3, 1), "frac_hbm": round(mb / mt / 1e3 / HBM_PEAK_GBS, 4),
                          "us_per_layer": round(mt, 3), "ceiling_us_per_layer": round(mp, 3),
                          "frac_of_ceiling": round(mp / mt, 4), "linears": lin}
-    # The dominant kernel is the one with the most time in the step.
-    dom = max(per_kernel, key=lambda k: per_kernel[k]["us"])
+    # The dominant kernel is the one that moves the most of the step's
+    # algorithmic bytes.  (Not the most event-timed time: a split-K GEMM on
+    # the tiled kernels also runs splitk_reduce_kernel, whose time the events
+    # around the GEMM include, so its kernel would be charged for both.)
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["bytes"])
     d = per_kernel[dom]
     achieved = d["bytes"] / d["us"] / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
