@@ -132,3 +132,49 @@ def test_counters_shared_across_shapes_and_graph_replays():
         for out, (M, K, N, *_, ref) in zip(outs, runs):
             assert torch.equal(out, ref), (rep, M, K, N)
     assert ops.counters_settled(cnt)
+
+
+@pytest.mark.parametrize("case", ["fixup_last_arrival", "fixup_polls", "kslice"])
+def test_split_k_handoff_reads_this_launchs_partials(case, plan):
+    """Regression test of the split-K handoffs through plain stores (each arrival a release,
+    the reading workgroup an acquire): consecutive launches alternate two inputs on one
+    counters buffer and the shared split-K workspace, so a partial read before its store
+    became visible would be the previous launch's, from the other input.  Every output must
+    equal the second-kernel reduction of its own input bit for bit (the k-slice kernel: its
+    own first result for that input, which the CPU oracle checks)."""
+    ops = _ops()
+    if case == "kslice":
+        M, K, N, G, act = 32, 4096, 2560, 128, None
+        plan.set("kslice_variant", 142)
+    else:
+        M, K, N, G, act = (200, 4096, 2560, 64, None) if case == "fixup_last_arrival" else (64, 14336, 4096, 128, None)
+        plan.set("tiled_fixup", 1)
+        if case == "fixup_last_arrival":
+            plan.set("fixup_polls", 0)
+    info = ops.plan_info(M, N, K, G, act)
+    print(f"case {case} M={M} K={K} N={N} G={G}: {info}", flush=True)
+    assert info.k_slices > 1
+    assert info.kernel == ("kslice_kernel" if case == "kslice" else "tiled_kernel")
+    if case != "kslice":
+        assert info.fixup
+    t = oracle.make_awq_linear(K, N, G, seed=K + N)
+    r = ops.repack(t["qweight"].to(DEV), t["qzeros"].to(DEV), t["scales"].to(DEV))
+    xs = [oracle.make_activation(M, K, seed=s) for s in (11, 12)]
+    cnt = ops.make_counters(N, DEV)
+    if case == "kslice":
+        refs = [ops.gemm(x.to(DEV), r, K, N, G, counters=cnt) for x in xs]
+    else:
+        plan.set("tiled_fixup", 0)
+        refs = [ops.gemm(x.to(DEV), r, K, N, G) for x in xs]
+        plan.set("tiled_fixup", 1)
+    torch.cuda.synchronize()
+    xd = [x.to(DEV) for x in xs]
+    outs = [ops.gemm(xd[i % 2], r, K, N, G, counters=cnt) for i in range(40)]
+    torch.cuda.synchronize()
+    for i, y in enumerate(outs):
+        assert torch.equal(y, refs[i % 2]), (case, i)
+    assert ops.counters_settled(cnt)
+    rows = sorted(set(range(8)) | set(range(M - 8, M)))
+    for x, ref in zip(xs, refs):
+        ok, err, mx = oracle.tolerance_ok(ref[rows], oracle.awq_gemm(x[rows], t["qweight"], t["qzeros"], t["scales"], None, G), TOL)
+        assert ok, (case, err, mx)
