@@ -6,6 +6,9 @@
 // 160 column tiles) split K across workgroups.  Summing the k-slices in a
 // second kernel costs a launch, about as long as a narrow layer's whole weight
 // stream; here the last workgroup of each column group to finish sums them.
+// The release/acquire pair that handoff needs costs about as much as the launch
+// it saves, so the planner does not choose this kernel; the planner override
+// (AWQ_PLAN_KSLICE_VARIANT) does.
 //
 // Workgroup: 4 waves = WN column waves x WK k-waves.  A wave owns 64 output
 // columns (two groups of 32 in the 32x32x16 operand order, WStage32) and KPW
