@@ -179,6 +179,17 @@ int gemv_default_variant(const Geom& g, int act) {
   return (k3 > 0 && (k4 == 0 || k3 <= k4)) ? v3 : v4;
 }
 
+// 17-32 rows with K of 17-24 k-tiles on layers of >= 384 column tiles, where
+// the GEMV kernel's default plan stages the whole activation slice unsplit
+// (at most 8 loads per thread): its two-tile (or six-tile) workgroups beat the
+// tiled kernel there (Qwen3-4B qkv at M = 24: 11.1 -> 8.6 us, at M = 25: 11.2
+// -> 8.8 us).  Beyond that the slice needs a K split and the tiled kernel wins.
+bool gemv_unsplit_short_k(const Geom& g) {
+  if (g.M <= 16 || g.M > 32 || g.KT <= 16 || g.KT > 24 || g.NT < 384) return false;
+  const int v = gemv_default_variant(g, 0);
+  return gemv_split(g, v, gemv_min_ks(g, v)).ks == 1;
+}
+
 // Where the GEMV kernel wins over the decode (skinny) kernel, from a
 // graph-replay sweep of M = 1..16 over the Qwen3-4B, Llama-3-8B and
 // Llama-3-70B projections on MI355X:
@@ -189,7 +200,8 @@ int gemv_default_variant(const Geom& g, int act) {
 //    k-tiles, and wherever the activation slice would cut a workgroup's K
 //    range to 16 k-tiles or fewer (2 per wave): there the workgroup's staged
 //    activation slice costs more than the skinny kernel's per-wave fragments;
-//  * 17-24 rows with short K on layers of >= 384 column tiles (below).
+//  * 17-32 rows with short K on layers of >= 384 column tiles whose
+//    activation slice it stages unsplit (gemv_unsplit_short_k).
 // A fused gate/up activation keeps the GEMV kernel up to 4 rows, and up to 8
 // rows when K fits in 24 k-tiles.
 bool gemv_preferred(const Geom& g, int act) {
@@ -203,11 +215,7 @@ bool gemv_preferred(const Geom& g, int act) {
   // GEMV kernel's two-tile workgroups win (1024 x 8192 at M = 32: 7.6 -> 6.7 us).
   if (g.KT <= 8) return g.M > 16 && g.NT >= 384;
   if (g.M <= 4) return g.M <= 2 || g.NT < 2048;
-  // 17-24 rows with K of 17-24 k-tiles on layers of >= 384 column tiles: the
-  // GEMV kernel's two-tile (or six-tile) workgroups stage the short
-  // activation slice once and beat the tiled kernel (Qwen3-4B qkv at M = 24:
-  // 11.1 -> 8.6 us); from 25 rows the tiled kernel wins.
-  if (g.M > 16) return g.M <= 24 && g.KT > 16 && g.KT <= 24 && g.NT >= 384;
+  if (g.M > 16) return gemv_unsplit_short_k(g);
   // Fewer than 128 column tiles, up to 8 rows: the skinny kernel would split
   // K to fill the CUs (4096 x 1536 at M = 8: 9.0 -> 6.8 us on the GEMV
   // kernel, K unsplit); from 12 rows the skinny kernel's 16-wave workgroups
@@ -256,7 +264,7 @@ bool plan_gemv(const Geom& g, GemmPlan& p, int act) {
 //    gate_up and down run 8-15% faster, e.g. 29.1 -> 24.7 us for a
 //    4096 x 28672 gate_up; the o_proj shapes stay 8-15% faster on the decode
 //    kernel), and the narrow deep layers below, except short K on wide
-//    layers up to 24 rows (the GEMV kernel's);
+//    layers whose activation slice the GEMV kernel stages unsplit;
 //  * 10-16 rows: K >= 8192 and K * N >= 40M (14336 x 4096 down: 19.4 ->
 //    15.4 us at M = 16; 28672 x 8192 down: 67.7 -> 37.3 us);
 //  * 5-9 rows: K >= 8192 and 4096 <= N < 32768 (the 70B qkv, o and down
@@ -279,7 +287,7 @@ bool tiled_preferred(const Geom& g, int act) {
   // at M = 32: 12.1 -> 11.5 us).
   const bool narrow_deep = (g.KT >= 48 && g.NT <= 256) || (g.KT >= 32 && g.NT < 128);
   if (g.M > 16) {
-    if (g.M <= 24 && g.KT > 16 && g.KT <= 24 && g.NT >= 384) return false;  // the GEMV kernel's
+    if (gemv_unsplit_short_k(g)) return false;  // the GEMV kernel's
     return (kn >= 12000000 && (g.N >= 6144 || g.K >= 8192)) || narrow_deep || (g.M >= 28 && g.KT >= 32 && g.NT <= 256);
   }
   // (9-16 rows: K of at most 31 k-tiles stays on the GEMV kernel, whose

@@ -103,7 +103,8 @@ def test_decode_routing(K, N, routes):
 
 def test_routing_at_17_to_32_rows():
     """17-32 rows: short K on layers of >= 384 column tiles stays on the GEMV
-    kernel up to 24 rows; narrow layers with deep K (>= 48 k-tiles, or >= 32
+    kernel while its activation slice fits unsplit (25 rows on the Qwen3-4B
+    qkv, 24 on its gate_up); narrow layers with deep K (>= 48 k-tiles, or >= 32
     on < 128 column tiles) split K on the 32-row tiled kernel; o_proj-shaped
     layers (32 k-tiles, <= 256 column tiles) keep the skinny kernel up to 27
     rows.  The planner never picks the k-slice kernel; the override does."""
@@ -111,7 +112,10 @@ def test_routing_at_17_to_32_rows():
         assert ops.gemm_kernel(M, 6144, 2560, 128) == "gemv_kernel"
         assert ops.gemm_kernel(M, 19456, 2560, 128) == "gemv_kernel"
         assert ops.gemm_kernel(M, 2560, 4096, 128) == "skinny_kernel"
-    for M in (25, 28, 32):
+    assert ops.gemm_kernel(25, 6144, 2560, 128) == "gemv_kernel"
+    assert ops.workspace_bytes(25, 6144, 2560, 128) == 0
+    assert ops.gemm_kernel(25, 19456, 2560, 128) == "tiled_kernel"
+    for M in (26, 28, 32):
         assert ops.gemm_kernel(M, 6144, 2560, 128) == "tiled_kernel"
     for M in (28, 32):
         assert ops.gemm_kernel(M, 2560, 4096, 128) == "tiled_kernel"
