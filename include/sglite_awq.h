@@ -256,7 +256,8 @@ int64_t awq_gated_mlp_take_errors(int32_t* counters, int64_t counter_bytes, awq_
  *                            G >= 64)
  *   AWQ_PLAN_TILED_KS        tiled k-slices
  *   AWQ_PLAN_KSLICE_VARIANT  k-slice decode-kernel shape wn*100 + wk*10 + kpw
- *                            (M <= 32; any other value leaves the plan alone)
+ *                            (M <= 32; any other value leaves the plan alone;
+ *                            the planner itself does not choose this kernel)
  *   AWQ_PLAN_TILED_FIXUP     1: split-K tiled plans sum their k-slices inside
  *                            the GEMM kernel when the counters are given
  *                            (default 0: in a second kernel)
