@@ -680,10 +680,177 @@ def _launches_per_call(ops, M: int, N: int, K: int, activation=None) -> int:
     return 2 if info.kernel == "tiled_kernel" and info.k_slices > 1 and not info.fixup else 1
 
 
+SQ_CASES = ([(f"Llama-3-8B {n} M=2048", 2048, K, N) for n, K, N in PREFILL]
+            + [("Llama-3-8B gate_up_proj M=8192", 8192, 4096, 28672)]
+            + [(f"Qwen3-4B {n} M={M}", M, K, N) for M in M_SET for n, K, N in LAYER])
+SQ_PASSES = (
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES SQ_WAIT_ANY "
+    "SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY GRBM_GUI_ACTIVE",
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_SCA "
+    "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE",
+    "SQ_WAVES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS SQ_INSTS_VMEM SQ_INSTS_SALU SQ_INSTS_SMEM SQ_WAIT_INST_LDS",
+)
+SQ_DENSE = [("hipBLASLt dense fp16 gate_up_proj M=2048", 2048, 4096, 28672),
+            ("hipBLASLt dense fp16 gate_up_proj M=8192", 8192, 4096, 28672)]
+SQ_REPS = 3  # counted calls per case (after one warm-up)
+SQ_MIN_CLOCK_US = 50.0  # shorter dispatches: GRBM_GUI_ACTIVE also counts the dispatch's set-up and drain
+MFMA_PEAK_GHZ = 2.4  # engine clock of the 2.5 PFLOP/s dense fp16 figure
+
+
+def sq_workload(ops, dev: torch.device, gen: torch.Generator) -> None:
+    """Launch sequence for the SQ-counter passes: the MFMA probe at one and two waves per SIMD, every
+    SQ_CASES GEMM, then the SQ_DENSE dense fp16 GEMMs (1 warm-up + SQ_REPS calls each, eager, in order)."""
+    sink = torch.empty(4 * 2 * ops.device_cu_count(), dtype=torch.float32, device=dev)
+    for grid in probe_grids(ops).values():
+        for _ in range(1 + SQ_REPS):
+            ops.mfma_probe(PROBE_ITERS, grid, 256, sink)
+    torch.cuda.synchronize()
+    for _, M, K, N in SQ_CASES:
+        r = make_repacked(ops, K, N, gen, dev)
+        cnt = ops.make_counters(N, dev)
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.float16)
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for _ in range(1 + SQ_REPS):
+            ops.gemm(x, r, K, N, G, counters=cnt, out=out)
+        torch.cuda.synchronize()
+        del r, x, out
+    for _, M, K, N in SQ_DENSE:  # the vendor library's dense GEMM on fp16 weights of the same shape
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.float16)
+        w = (torch.randn((K, N), generator=gen, device=dev) * 0.02).to(torch.float16)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(1 + SQ_REPS):
+            torch.matmul(x, w, out=y)
+        torch.cuda.synchronize()
+        del x, w, y
+
+
+def sq_summary(dirs: list) -> str:
+    """Markdown summary of the SQ-counter passes (one rocprofv3 --pmc run of `--profile-workload sq` per
+    SQ_PASSES entry).  Counters are summed over the device by rocprofv3; each case's row is the mean over
+    its counted calls (the warm-up call is dropped), matched by kernel function, grid and block from
+    ops.plan_info.  Wave-time fractions divide SQ_WAIT_* / SQ_ACTIVE_INST_* by SQ_WAVE_CYCLES (all in
+    quad-cycles, summed over waves); MFMA and VALU busy divide the per-SIMD busy cycles by the SIMD count
+    times the kernel's cycles (GRBM_GUI_ACTIVE, counted per XCD, over the XCD count); the MFMA probe,
+    which issues nothing but independent MFMAs, calibrates the MFMA figure."""
+    from collections import defaultdict
+    from sglite_amd import ops
+
+    cus = ops.device_cu_count()
+    simds, xcds = 4 * cus, max(1, cus // 32)
+    # The workload's engine dispatches in order: (function, workgroups, block) per case, 1 + SQ_REPS each.
+    plan = [(f"MFMA probe, {label.replace('_', ' ')}", "mfma_probe_kernel", grid, 256)
+            for label, grid in probe_grids(ops).items()]
+    for label, M, K, N in SQ_CASES:
+        info = ops.plan_info(M, N, K, G)
+        plan.append((label, info.function, info.workgroups, info.threads))
+    plan += [(label, "Cijk_", 0, 0) for label, *_ in SQ_DENSE]  # hipBLASLt kernels: matched by name prefix
+    counted = [defaultdict(list) for _ in plan]  # per case: counter -> values of its counted calls
+    kernels = [""] * len(plan)
+    for d in dirs:
+        disp = {}
+        for r in _pmc_rows(d):
+            name = r["Kernel_Name"]
+            short = name.replace("(anonymous namespace)::", "").replace("sgl_awq::", "").replace("void ", "")
+            short = short[:short.index("(")] if "(" in short else short
+            bx = int(r["Workgroup_Size"])  # counter-collection rows give total sizes (work-items)
+            e = disp.setdefault(int(r["Dispatch_Id"]), [(short, int(r["Grid_Size"]) // bx, bx), {}])
+            e[1][r["Counter_Name"]] = float(r["Counter_Value"])
+            e[1]["duration_ns"] = float(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        seq = [disp[i] for i in sorted(disp)]
+        pos = 0
+        for ci, (_, fn, wgs, block) in enumerate(plan):
+            got = 0
+            while pos < len(seq) and got < 1 + SQ_REPS:
+                (short, w, b), cs = seq[pos]
+                pos += 1
+                if fn == "Cijk_":
+                    hit = short.startswith(fn)
+                else:
+                    hit = (short == fn or short.startswith(fn + "<")) and w == wgs and b == block
+                if hit:
+                    if got > 0:  # the first call is the warm-up
+                        for c, v in cs.items():
+                            counted[ci][c].append(v)
+                    kernels[ci] = short
+                    got += 1
+
+    def div(a: float, b: float) -> float:
+        return a / b if b else float("nan")
+
+    def metrics(cs: dict) -> dict:
+        g = lambda n: sum(cs[n]) / len(cs[n]) if cs.get(n) else float("nan")
+        cyc = g("GRBM_GUI_ACTIVE") / xcds
+        wc = g("SQ_WAVE_CYCLES")
+        waves = g("SQ_WAVES")
+        us = g("duration_ns") / 1e3
+        ghz = cyc / (us * 1e3) if us >= SQ_MIN_CLOCK_US else float("nan")
+        mfma = div(g("SQ_VALU_MFMA_BUSY_CYCLES"), simds * cyc)
+        return {
+            "us": us, "ghz": ghz, "rate": mfma * ghz / MFMA_PEAK_GHZ,
+            "mfma": mfma,
+            "valu": div(4 * g("SQ_ACTIVE_INST_VALU"), simds * cyc),
+            "coexec": div(g("SQ_VALU_MFMA_COEXEC_CYCLES"), g("SQ_VALU_MFMA_BUSY_CYCLES")),
+            "w_issue": div(g("SQ_WAIT_INST_ANY"), wc), "w_any": div(g("SQ_WAIT_ANY"), wc),
+            "a_any": div(g("SQ_ACTIVE_INST_ANY"), wc), "a_valu": div(g("SQ_ACTIVE_INST_VALU"), wc),
+            "a_lds": div(g("SQ_ACTIVE_INST_LDS"), wc), "a_vmem": div(g("SQ_ACTIVE_INST_VMEM"), wc),
+            "a_sca": div(g("SQ_ACTIVE_INST_SCA"), wc),
+            "conflict": div(g("SQ_LDS_BANK_CONFLICT"), g("SQ_LDS_IDX_ACTIVE")),
+            "i_valu": div(g("SQ_INSTS_VALU"), waves), "i_mfma": div(g("SQ_INSTS_MFMA"), waves),
+            "i_lds": div(g("SQ_INSTS_LDS"), waves), "i_vmem": div(g("SQ_INSTS_VMEM"), waves),
+            "i_salu": div(g("SQ_INSTS_SALU") + g("SQ_INSTS_SMEM"), waves),
+        }
+
+    cases = [(plan[i][0], kernels[i] if plan[i][1] != "Cijk_" else kernels[i][:40] + "...", metrics(counted[i]))
+             for i in range(len(plan)) if kernels[i]]
+    f = lambda v, d=2: "n/a" if v != v else f"{v:.{d}f}"
+    lines = [
+        "# SQ counters of the prefill and decode kernels (rocprofv3 --pmc), with the MFMA probe", "",
+        "Commands (from the repository root, TMPDIR=/tmp), one counter set per run:", ""]
+    for i, p in enumerate(SQ_PASSES):
+        lines.append(f"    rocprofv3 --pmc {p} -f csv -d <dir{i + 1}> -o pmc -- python3 bench.py --profile-workload sq")
+    lines += [f"    python3 bench.py --sq-summary <dir1> <dir2> <dir3>", "",
+              "Workload: the MFMA probe (eight independent 32x32x16 fp16 MFMAs per wave, no memory traffic) at one",
+              "and two waves per SIMD, the Llama-3-8B linears at M = 2048, its gate_up at M = 8192, and the",
+              f"Qwen3-4B decode linears at M = 1, 8, 32; fp16, int4 group 128; then the vendor library's dense fp16 "
+              "GEMM (torch.matmul, hipBLASLt) on fp16 weights of the Llama-3-8B gate_up shape at M = 2048 and 8192.",
+              f"Each case 1 warm-up + {SQ_REPS} counted calls (dispatches are serialised under counter collection).",
+              "",
+              "* us: mean dispatch duration under counter collection.  Clock: kernel cycles (GRBM_GUI_ACTIVE / XCDs)",
+              f"  over that duration, shown for dispatches of at least {SQ_MIN_CLOCK_US:.0f} us (shorter ones are "
+              "dominated by set-up and drain).",
+              "* MFMA busy: SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x kernel cycles) "
+              f"({simds} SIMDs, {xcds} XCDs); times clock / 2.4 GHz it estimates the",
+              "  fraction of the 2.5 PFLOP/s dense fp16 peak (the probe's estimate matches its timed rate).",
+              "  VALU busy: 4 x SQ_ACTIVE_INST_VALU over the same.",
+              "* co-exec: SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES (MFMA-busy cycles in which a VALU",
+              "  instruction also issued).",
+              "* wait issue / wait any / active: SQ_WAIT_INST_ANY, SQ_WAIT_ANY and SQ_ACTIVE_INST_{ANY,VALU,LDS,VMEM,SCA}",
+              "  over SQ_WAVE_CYCLES (fractions of the waves' resident time; categories overlap).",
+              "* LDS conflict: SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE.  Instructions per wave: SQ_INSTS_* / SQ_WAVES",
+              "  (SALU includes SMEM).",
+              "",
+              "| case | kernel | us | clock GHz | MFMA busy | MFMA busy x clock / 2.4 GHz | VALU busy | co-exec | "
+              "wait issue | wait any | active any | active VALU | active LDS | active VMEM | active SALU | "
+              "LDS conflict | VALU / MFMA / LDS / VMEM / SALU instructions per wave |",
+              "|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for label, kern, m in cases:
+        lines.append(
+            f"| {label} | `{kern}` | {f(m['us'], 1)} | {f(m['ghz'])} | {f(m['mfma'])} | {f(m['rate'])} | "
+            f"{f(m['valu'])} | {f(m['coexec'])} | {f(m['w_issue'])} | "
+            f"{f(m['w_any'])} | {f(m['a_any'])} | {f(m['a_valu'])} | {f(m['a_lds'])} | {f(m['a_vmem'])} | "
+            f"{f(m['a_sca'])} | {f(m['conflict'], 3)} | {f(m['i_valu'], 0)} / {f(m['i_mfma'], 0)} / "
+            f"{f(m['i_lds'], 0)} / {f(m['i_vmem'], 0)} / {f(m['i_salu'], 0)} |")
+    return "\n".join(lines) + "\n"
+
+
 def profile_workload(name: str, ops, dev: torch.device, gen: torch.Generator) -> None:
     """A fixed launch sequence for `rocprofv3 --kernel-trace` (one section of the benchmark, eager calls
-    in a known order), read back by --rocprof-summary NAME."""
-    if name.startswith("prefill"):
+    in a known order), read back by --rocprof-summary NAME; `sq` is the SQ-counter workload
+    (--sq-summary)."""
+    if name == "sq":
+        sq_workload(ops, dev, gen)
+    elif name.startswith("prefill"):
         M = int(name.split("-")[1])
         x = {K: torch.randn((M, K), generator=gen, device=dev).to(torch.float16) for K in {k for _, k, _ in PREFILL}}
         for lname, K, N in PREFILL:
@@ -1214,11 +1381,14 @@ def main() -> int:
                     help="the profiled command, quoted in the summary's header")
     ap.add_argument("--profile-workload", metavar="NAME",
                     help="run one section's launch sequence for rocprofv3 --kernel-trace and exit: prefill-2048, "
-                         "prefill-8192, moe, stack70b-64, stack70b-4096, mlp or probes")
+                         "prefill-8192, moe, stack70b-64, stack70b-4096, mlp, probes, or sq (the SQ-counter workload)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run each decode GEMM of the step a few times eagerly plus a 256 MiB copy, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="print a markdown summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of --pmc-workload")
+    ap.add_argument("--sq-summary", nargs="+", metavar="PMC_DIR",
+                    help="print a markdown summary of the SQ-counter passes (rocprofv3 --pmc of --profile-workload sq, "
+                         "one directory per counter set) and exit")
     ap.add_argument("--marker-summary", metavar="TRACE_DIR",
                     help="print a markdown summary of a rocprofv3 --marker-trace --kernel-trace run (the C ABI's "
                          "roctx ranges) and exit")
@@ -1232,6 +1402,9 @@ def main() -> int:
         return 0
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary), end="")
+        return 0
+    if args.sq_summary:
+        print(sq_summary(args.sq_summary), end="")
         return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the engine's multi-GPU sharding is a "
