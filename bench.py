@@ -682,7 +682,8 @@ def _launches_per_call(ops, M: int, N: int, K: int, activation=None) -> int:
 
 SQ_CASES = ([(f"Llama-3-8B {n} M=2048", 2048, K, N) for n, K, N in PREFILL]
             + [("Llama-3-8B gate_up_proj M=8192", 8192, 4096, 28672)]
-            + [(f"Qwen3-4B {n} M={M}", M, K, N) for M in M_SET for n, K, N in LAYER])
+            + [(f"Qwen3-4B {n} M={M}", M, K, N) for M in M_SET for n, K, N in LAYER]
+            + [(f"Llama-3-8B {n} M={M}", M, K, N) for M in (64, 256) for n, K, N in PREFILL])
 SQ_PASSES = (
     "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_VALU_MFMA_COEXEC_CYCLES SQ_WAIT_ANY "
     "SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY GRBM_GUI_ACTIVE",
@@ -805,14 +806,15 @@ def sq_summary(dirs: list) -> str:
              for i in range(len(plan)) if kernels[i]]
     f = lambda v, d=2: "n/a" if v != v else f"{v:.{d}f}"
     lines = [
-        "# SQ counters of the prefill and decode kernels (rocprofv3 --pmc), with the MFMA probe", "",
+        "# SQ counters of the prefill, mid-size and decode kernels (rocprofv3 --pmc), with the MFMA probe", "",
         "Commands (from the repository root, TMPDIR=/tmp), one counter set per run:", ""]
     for i, p in enumerate(SQ_PASSES):
         lines.append(f"    rocprofv3 --pmc {p} -f csv -d <dir{i + 1}> -o pmc -- python3 bench.py --profile-workload sq")
     lines += [f"    python3 bench.py --sq-summary <dir1> <dir2> <dir3>", "",
               "Workload: the MFMA probe (eight independent 32x32x16 fp16 MFMAs per wave, no memory traffic) at one",
               "and two waves per SIMD, the Llama-3-8B linears at M = 2048, its gate_up at M = 8192, and the",
-              f"Qwen3-4B decode linears at M = 1, 8, 32; fp16, int4 group 128; then the vendor library's dense fp16 "
+              f"Qwen3-4B decode linears at M = 1, 8, 32, the Llama-3-8B linears at M = 64 and 256; fp16, int4 group "
+              "128; then the vendor library's dense fp16 "
               "GEMM (torch.matmul, hipBLASLt) on fp16 weights of the Llama-3-8B gate_up shape at M = 2048 and 8192.",
               f"Each case 1 warm-up + {SQ_REPS} counted calls (dispatches are serialised under counter collection).",
               "",
