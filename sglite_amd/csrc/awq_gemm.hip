@@ -1,13 +1,15 @@
 // W4A16 GEMM planning and dispatch for gfx950: out[M, N] = x[M, K] @ W
 // (+ bias), fp32 accumulation, optionally with the gated activation of a
 // merged gate/up projection fused (out[M, N / 2] = act(gate) * up).  Four
-// kernels share the CDNA4 tile layout (awq_device.h):
+// kernel kinds share the CDNA4 tile layout (awq_device.h):
 //
 //  * gemv_kernel (awq_gemv.hip): batches of a few rows, HBM-bound;
 //  * skinny_kernel (awq_skinny.hip): decode batches up to 32 rows, HBM-bound
 //    split-K;
-//  * tiled_kernel (awq_tiled.hip): prefill (MFMA-bound) and 16-32 rows on
-//    large matrices, split K through a second reduction kernel;
+//  * the tiled kind (awq_tiled.hip: tiled_kernel on 16x16x32 MFMAs,
+//    mfma32_kernel on 32x32x16 ones): prefill (MFMA-bound), mid-size batches
+//    and 5-32 rows on large or deep matrices, split K summed by a second
+//    reduction kernel (or, on request, inside the GEMM kernel);
 //  * kslice_kernel (awq_kslice.hip): decode batches up to 32 rows, split K
 //    reduced by the last workgroup of each column group (planner override
 //    only).
