@@ -1357,6 +1357,33 @@ def planner_sweep(ops, dev, groups, Ms) -> None:
                 torch.cuda.empty_cache()
 
 
+def headline_summary(dec, prefill, moe, llama, stack, mlp, bounds) -> dict:
+    """The sections' key figures in a few hundred characters, printed last on the JSON line so that a
+    log that keeps only the end of the line still holds them: per decode batch [us per layer, fraction
+    of the streaming ceiling, GB/s]; per Llama-3-8B batch [us per layer, fraction of the roofline its
+    arithmetic intensity puts it under]; prefill, MoE, 70B-stack, gated-MLP and bound fractions."""
+    out: dict = {}
+    if dec is not None:
+        out["decode_per_m"] = {M: [v["us_per_layer"], v["frac_of_ceiling"], v["GB/s"]] for M, v in dec["per_m"].items()}
+    if prefill is not None:
+        out["prefill_frac"] = {"2048": prefill["frac"], "8192": prefill["m8192"]["frac"]}
+    if moe is not None:
+        out["moe"] = [moe["us"], moe["frac"]]
+    if llama is not None:
+        out["llama3_8b"] = {M: [v["us_per_layer"], v["frac_hbm"] if v["bound"] == "hbm" else v["frac_mfma"]]
+                            for M, v in llama["per_m"].items()}
+    if stack is not None:
+        out["stack70b"] = {M: v["frac_hbm"] if M == "64" else v["frac_mfma"] for M, v in stack["per_m"].items()}
+    if mlp is not None:
+        out["gated_mlp_fused_us"] = {M: v["fused_us"] for M, v in mlp["per_m"].items()}
+    if bounds is not None:
+        out["mfma_probe_frac"] = [bounds[k]["frac"] for k in ("1_wave_per_simd", "2_waves_per_simd") if k in bounds]
+        hb = bounds.get("hipblaslt_dense_fp16")
+        if hb:
+            out["hipblaslt_frac"] = {M: hb[M]["frac"] for M in ("2048", "8192") if M in hb}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1540,6 +1567,7 @@ def main() -> int:
         "prefill": prefill,
         "decode_kernels": None if dec is None else dec["kernels"],
         "per_m": None if dec is None else dec["per_m"],
+        "summary": headline_summary(dec, prefill, moe, llama, stack, mlp, bounds),
     }
     print(json.dumps(line))
     return 0
