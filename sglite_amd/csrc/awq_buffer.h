@@ -25,6 +25,8 @@ constexpr int kCacheStream = 2;
 // outstanding and leaves the other counters alone (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+// The same with no LDS operation outstanding either (lgkmcnt 0).
+constexpr int vmcnt_lgkm0_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
 
 // Handoff of plain stores between the workgroups of one launch (possibly on
 // different XCDs, whose L2s are made coherent only by explicit writeback and

@@ -339,8 +339,17 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   };
   // Every wave's activation loads of k-tile kt + 1 have landed, and every
   // wave is done reading the buffer that the next activation load refills.
-  auto sync_step = [&]() {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterX));
+  // The wait includes the LDS reads (lgkmcnt 0): block 3's operand reads and
+  // the chunk reads are issued before the barrier but consumed after it, and
+  // a barrier does not wait for them, while other waves refill that buffer
+  // after it.  `drain` (the steps after the counted loop) waits for every
+  // load: there the prefetches past the k-slice have no use, the compiler
+  // removes their weight loads, and fewer loads follow k-tile kt + 1's
+  // activations than kAfterX counts (with NS = 3 the last k-tile of a slice
+  // was then multiplied with activation fragments that had not all landed).
+  auto sync_step = [&](bool drain) {
+    if (drain) __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(kAfterX));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   // that ends chunk ci's last read (the first step's weight issue), and ahead
   // of the activation loads that the wait before its own first read (the
   // next iteration's second step) covers.
-  auto step = [&](int p, int kt) {
+  auto step = [&](int p, int kt, bool drain) {
     const int pa = (p + NS - 1) % NS, pn = (p + 1) % NS;
     const int ka = kt + NS - 1;
     if constexpr (kZsLds) {
@@ -372,14 +381,14 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     load_w(st[pa], ka);  // the wait counts rely on this issue order
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kZsLds) {
-      // Issued before the next LDS reads, whose waits then cover them before
-      // the barrier after which a chunk buffer may be refilled.
+      // Complete at the next barrier (sync_step waits for the LDS reads), after
+      // which a chunk buffer may be refilled.
       read_zs(st[pa], ka);
       __builtin_amdgcn_sched_barrier(0);
     }
     fetch(1, st[p], xbuf(p), 3);
     mma(0);
-    sync_step();
+    sync_step(drain);
     make_zs(st[pn]);
     fetch(0, st[pn], xbuf(pn), 0);
     mma(1);
@@ -399,7 +408,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
     load_w(st[p], kt0 + p);
     __builtin_amdgcn_sched_barrier(0);
   }
-  sync_step();
+  sync_step(false);
   if constexpr (kZsLds) {
 #pragma unroll
     for (int p = 0; p + 1 < NS; ++p) read_zs(st[p], kt0 + p);
@@ -414,11 +423,11 @@ __global__ __launch_bounds__(256) void tiled_kernel(TiledArgs a) {
   int i = 0;
   for (; i + NS <= nsteps; i += NS) {
 #pragma unroll
-    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p);
+    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p, false);
   }
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p)
-    if (i + p < nsteps) step(p, kt0 + i + p);
+    if (i + p < nsteps) step(p, kt0 + i + p, true);
 
   // The last steps prefetched past the end; no load may still be writing
   // this workgroup's LDS when it exits.
@@ -800,8 +809,14 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
       }
     }
   };
-  auto sync_step = [&]() {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAfterX));
+  // As in tiled_kernel: the wait covers the LDS reads as well (the compiler
+  // moves a k-tile's last MFMAs, and the operand reads they consume, past the
+  // barrier, after which other waves refill that buffer), and the steps after
+  // the counted loop, whose useless weight prefetches the compiler removes,
+  // wait for every load.
+  auto sync_step = [&](bool drain) {
+    if (drain) __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(kAfterX));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
@@ -825,12 +840,12 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
     load_w(stg[p], kt0 + p);
     __builtin_amdgcn_sched_barrier(0);
   }
-  sync_step();
+  sync_step(false);
   if constexpr (kZsLds) {
 #pragma unroll
     for (int p = 0; p + 1 < NS; ++p) read_zs(stg[p], kt0 + p);
   }
-  auto step = [&](int p, int kt) {
+  auto step = [&](int p, int kt, bool drain) {
     const int pa = (p + NS - 1) % NS;
     if constexpr (kZsLds) {
       if (p == 1) dma_chunk((kt - 1 - kt0) / NS + 2);
@@ -853,23 +868,23 @@ __global__ __launch_bounds__(64 * NW, OCC) void mfma32_kernel(TiledArgs a) {
       load_w(stg[pa], kt + NS - 1);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (kZsLds) {
-        // Issued before the compute's LDS reads, whose waits then cover them
-        // before the barrier after which a chunk buffer may be refilled.
+        // Complete at the next barrier (sync_step waits for the LDS reads),
+        // after which a chunk buffer may be refilled.
         read_zs(stg[pa], kt + NS - 1);
         __builtin_amdgcn_sched_barrier(0);
       }
       compute(stg[p], xbuf(p), [](int) {});
     }
-    sync_step();
+    sync_step(drain);
   };
   int i = 0;
   for (; i + NS <= nsteps; i += NS) {
 #pragma unroll
-    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p);
+    for (int p = 0; p < NS; ++p) step(p, kt0 + i + p, false);
   }
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p)
-    if (i + p < nsteps) step(p, kt0 + i + p);
+    if (i + p < nsteps) step(p, kt0 + i + p, true);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   if constexpr (KW == 2) {
     // k-wave 1 hands its accumulators to k-wave 0 one column group at a time
