@@ -47,7 +47,7 @@ enum { AWQ_DTYPE_FP16 = 0, AWQ_DTYPE_BF16 = 1 };
 /* Message of the last failed call on this thread ("" if none). */
 const char* awq_last_error(void);
 
-/* Library version string, e.g. "sglite-awq-gfx950 0.3". */
+/* Library version string, e.g. "sglite-awq-gfx950 0.4". */
 const char* awq_version(void);
 
 /* ABI revision of this header.  A caller checks awq_abi_version() ==
