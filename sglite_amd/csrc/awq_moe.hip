@@ -562,21 +562,28 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
   };
   auto issue = [&](Stage& st) {
     dma_x(ik, islot);
+    __builtin_amdgcn_sched_barrier(0);
     load_w(iu, min(ik, KT - 1), st);
     advance();
   };
   Stage st[NS];
-  // The prologue issues in the steady-state order (an empty asm statement
-  // with a memory clobber keeps the compiler from grouping the loads by
-  // kind), so the waits the compiler derives for the loop hold from its first
-  // step.
+  // The prologue issues in the steady-state order: activation DMAs, then the
+  // weight, zero and scale loads, one step after the other.  The compiler's
+  // waits in the loop are derived from both ways into it, so a prologue that
+  // grouped the loads by kind (all steps' DMAs first, as the scheduler does
+  // across a mere memory clobber) would make the loop's first two steps wait
+  // for loads of the steps after them on every iteration.
 #pragma unroll
   for (int p = 0; p + 1 < NS; ++p) {
     issue(st[p]);
-    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
   }
   int cu = 0, ck = 0, cslot = 0;  // step being multiplied
-  for (int s = 0; s < nsteps; s += NS) {
+  // units >= 1 and KTp >= NS: the loop runs at least once, so its guard does
+  // not pull the prologue's weight loads below it (past the DMAs of the
+  // later steps).
+  int s = 0;
+  do {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       Stage& sn = st[(i + NS - 1) % NS];
@@ -611,7 +618,8 @@ __device__ __forceinline__ void moe_pass(const MoeArgs& a, u32x4* __restrict__ x
       ck = 0;
       ++cu;
     }
-  }
+    s += NS;
+  } while (s < nsteps);
 }
 
 // Balanced placement of the slice groups of one XCD.  Launched on an idle
