@@ -447,7 +447,10 @@ def test_every_tiled_variant(bm, G, dtype, plan):
     k-tile x dtype): K with a partial last k-tile (and, for G < 128, groups
     past K inside it), N % 256 != 0 with N % 16 == 8, and row counts that
     leave the last row block partial; whole pipeline rounds plus a
-    remainder, with and without split K."""
+    remainder, with and without split K.  The k-slice counts give slices of
+    19 (unsplit), 7, 4 and 2 k-tiles with last slices of 5, 3 and 1 (for
+    G = K: 9, 3, 2 and 1): every length modulo the 2- to 5-stage pipelines,
+    and slices shorter than the prologue."""
     ops = _ops()
     K = {32: 2336, 64: 2368, 128: 2432, -1: 1120}[G]
     N = 264
@@ -456,14 +459,16 @@ def test_every_tiled_variant(bm, G, dtype, plan):
     cnt = ops.make_counters(N, DEV)
     plan.set("tiled_bm", str(bm))
     plan.set("tiled_min_m", "1")  # small batches through this kernel too
-    for ks in (1, 3):  # whole K per workgroup, and three k-slices
+    xs = {M: oracle.make_activation(M, K, seed=M + bm, dtype=dtype) for M in (20, 33, 130, 257)}
+    refs = {M: oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G) for M, x in xs.items()}
+    for ks in (1, 3, 5, 10):  # whole K per workgroup, then slices of about 7, 4 and 2 k-tiles
         plan.set("tiled_ks", str(ks))
-        for M in (20, 33, 130, 257):
-            x = oracle.make_activation(M, K, seed=M + bm, dtype=dtype)
-            y = ops.gemm(x.to(DEV), r, K, N, G, counters=cnt)
-            ref = oracle.awq_gemm(x, t["qweight"], t["qzeros"], t["scales"], None, G)
-            ok, err, mx = oracle.tolerance_ok(y, ref, TOL)
+        for M, x in xs.items():
+            xd = x.to(DEV)
+            y = ops.gemm(xd, r, K, N, G, counters=cnt)
+            ok, err, mx = oracle.tolerance_ok(y, refs[M], TOL)
             assert ok, (bm, G, ks, M, err, mx)
+            assert torch.equal(ops.gemm(xd, r, K, N, G, counters=cnt), y), (bm, G, ks, M)  # a second call
     assert ops.counters_settled(cnt)
     assert ops.gemm_kernel(20, N, K, G) == "tiled_kernel"
 
